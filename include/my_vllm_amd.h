@@ -1,0 +1,104 @@
+/*
+ * C ABI of libmy_vllm_amd.so: gfx950 (MI355X) kernels for the ragged-batch
+ * attention hot path of Nano-vLLM-v1 and its SiLU-and-mul op.
+ *
+ * Conventions shared by every entry point:
+ *   - Buffers are raw device pointers; sizes and strides are int64 and count
+ *     ELEMENTS (not bytes) unless the name says otherwise.
+ *   - `dtype` is MVA_DTYPE_BF16 or MVA_DTYPE_F16 (storage type of activations
+ *     and of the KV cache; all arithmetic is fp32).
+ *   - `stream` is a hipStream_t (pass torch.cuda.current_stream().cuda_stream);
+ *     launches are asynchronous and no entry point synchronizes the device.
+ *   - Return 0 on success, a negative status otherwise; mva_last_error()
+ *     returns the calling thread's last message.  Nothing throws across the ABI.
+ *   - Load this library after the process's HIP runtime (torch's) is loaded,
+ *     so both bind to the same runtime instance.
+ */
+#ifndef MY_VLLM_AMD_H_
+#define MY_VLLM_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MVA_DTYPE_BF16 0
+#define MVA_DTYPE_F16 1
+
+/* Message of the calling thread's most recent failed call ("" if none). */
+const char* mva_last_error(void);
+
+/* ABI revision of this header. */
+int mva_abi_version(void);
+
+/*
+ * out[r, c] = silu(in[r, c]) * in[r, c + hidden] for r < rows, c < hidden.
+ * `input` is a contiguous [rows, 2*hidden] buffer, `output` a contiguous
+ * [rows, hidden] buffer; fp32 math, one rounding to `dtype`.
+ * Replaces the reference's `nanovllm._C.forward` (csrc/silu_and_mul.cpp:24-29,
+ * kernel csrc/silu_and_mul_kernel.cu:11-77), bound by
+ * nanovllm/layers/cuda_ops.py:29-34; the Python side keeps its argument
+ * checks and error messages (csrc/silu_and_mul.cpp:8-18).
+ */
+int mva_silu_and_mul(const void* input, void* output, int64_t rows, int64_t hidden, int dtype,
+                     void* stream);
+
+/*
+ * slot_mapping KV-cache store.  For each token t < num_tokens whose slot
+ * s = slot_mapping[t] satisfies 0 <= s < num_slots, copies row_elems elements
+ * of key + t*key_row_stride to k_cache + s*row_elems and of
+ * value + t*value_row_stride to v_cache + s*row_elems.  slot_mapping is int32,
+ * or int64 when slot_is_int64 != 0.  row_elems = num_kv_heads * head_dim;
+ * num_slots = num_pages * page_size.  Bit copy (no rounding).
+ * Replaces `store_kvcache` (nanovllm/layers/attention.py:34-41, Triton kernel
+ * :11-31) behind KVCacheStore (:44-101).
+ */
+int mva_kv_store(const void* key, int64_t key_row_stride, const void* value,
+                 int64_t value_row_stride, void* k_cache, void* v_cache, int64_t num_slots,
+                 const void* slot_mapping, int slot_is_int64, int64_t num_tokens, int64_t row_elems,
+                 int dtype, void* stream);
+
+/*
+ * Bytes of device workspace mva_paged_decode needs for `num_seqs` sequences
+ * and `num_part_slots` split-K partial slots.  The workspace must be zeroed
+ * once when first allocated; the kernels leave it zeroed again on return.
+ */
+int64_t mva_decode_workspace_bytes(int64_t num_seqs, int64_t num_part_slots, int num_kv_heads,
+                                   int group);
+
+/*
+ * Paged GQA decode (one query token per sequence) over an NHD page cache
+ * k_cache / v_cache = [num_pages, page_size, num_kv_heads, head_dim] with
+ * page_stride / token_stride element strides (head stride = head_dim).
+ *   q:    query rows; q + row*q_token_stride + head*q_head_stride.
+ *   block_tables [num_seqs, block_table_stride] int32 page ids; seq_lens
+ *         [num_seqs] int32 context lengths (including the new token).
+ *   items [num_items, 8] int32 work items, each
+ *         {seq, page_begin, page_end, chunk, n_chunks, part_base, q_row, 0}:
+ *         pages [page_begin, page_end) of sequence `seq` (at most 128 pages),
+ *         chunk `chunk` of `n_chunks`; partial slots part_base .. part_base +
+ *         n_chunks - 1 (unused when n_chunks == 1); output row q_row.
+ *   out:  out + row*out_token_stride + head*out_head_stride, `dtype`.
+ * softmax over keys j < seq_len with scale `softmax_scale`; fp32 accumulate.
+ * Launch grid = num_items x num_kv_heads wavefronts; split chunks are merged
+ * in the same launch.  Requires head_dim 128, page_size 16, num_q_heads /
+ * num_kv_heads <= 16, 16-byte aligned q/cache buffers and strides.
+ * Replaces FlashInfer BatchDecodeWithPagedKVCacheWrapper.plan/run as used by
+ * the reference's DECODE route (nanovllm/layers/attention_backend.py:826-840,
+ * :995-997) and the decode half of MIXED_SPLIT (:874-889, :1020-1025).
+ */
+int mva_paged_decode(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                     const void* k_cache, const void* v_cache, int64_t num_pages,
+                     int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
+                     int64_t block_table_stride, const int32_t* seq_lens, const int32_t* items,
+                     int64_t num_items, int64_t num_seqs, int64_t num_part_slots, void* out,
+                     int64_t out_token_stride, int64_t out_head_stride, void* workspace,
+                     int64_t workspace_bytes, int num_q_heads, int num_kv_heads, int head_dim,
+                     int page_size, float softmax_scale, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MY_VLLM_AMD_H_ */

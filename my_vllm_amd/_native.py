@@ -1,0 +1,115 @@
+"""ctypes binding of ``lib/libmy_vllm_amd.so`` (C ABI in ``include/my_vllm_amd.h``).
+
+The library is loaded lazily, after ``torch`` (whose bundled HIP runtime the
+library then binds to: both carry the soname ``libamdhip64.so.7``).  There is no
+fallback: when the library is missing every call raises ``RuntimeError`` naming
+the build command, so a GPU run can never silently use another implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libmy_vllm_amd.so"
+
+DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1}
+
+_c_void_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_f32 = ctypes.c_float
+
+# name -> (restype, argtypes); mirrors include/my_vllm_amd.h.
+_SIGNATURES = {
+    "mva_last_error": (ctypes.c_char_p, []),
+    "mva_abi_version": (_i32, []),
+    "mva_silu_and_mul": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _i32, _c_void_p]),
+    "mva_kv_store": (
+        _i32,
+        [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _i32, _i64, _i64, _i32, _c_void_p],
+    ),
+    "mva_decode_workspace_bytes": (_i64, [_i64, _i64, _i32, _i32]),
+    "mva_paged_decode": (
+        _i32,
+        [
+            _c_void_p, _i64, _i64,  # q, q_token_stride, q_head_stride
+            _c_void_p, _c_void_p, _i64, _i64, _i64,  # k_cache, v_cache, num_pages, page_stride, token_stride
+            _c_void_p, _i64, _c_void_p,  # block_tables, block_table_stride, seq_lens
+            _c_void_p, _i64, _i64, _i64,  # items, num_items, num_seqs, num_part_slots
+            _c_void_p, _i64, _i64,  # out, out_token_stride, out_head_stride
+            _c_void_p, _i64,  # workspace, workspace_bytes
+            _i32, _i32, _i32, _i32, _f32, _i32, _c_void_p,  # heads, head_dim, page, scale, dtype, stream
+        ],
+    ),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+_load_error: Exception | None = None
+
+
+def load_library() -> ctypes.CDLL:
+    """Load and type the shared library (once); raise RuntimeError if absent."""
+    global _lib, _load_error
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            _load_error = FileNotFoundError(str(LIB_PATH))
+            raise RuntimeError(
+                f"my_vllm_amd native library is missing ({LIB_PATH}); "
+                "build it with `python -m my_vllm_amd.build`"
+            )
+        try:
+            lib = ctypes.CDLL(str(LIB_PATH))
+        except OSError as error:
+            _load_error = error
+            raise RuntimeError(f"cannot load {LIB_PATH}: {error}") from error
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+        return lib
+
+
+def native_available() -> bool:
+    try:
+        load_library()
+    except RuntimeError:
+        return False
+    return True
+
+
+def call(name: str, *args) -> None:
+    """Call a status-returning entry point; map a nonzero status to RuntimeError."""
+    lib = load_library()
+    status = getattr(lib, name)(*args)
+    if status != 0:
+        message = lib.mva_last_error().decode("utf-8", "replace")
+        raise RuntimeError(f"{name} failed ({status}): {message}")
+
+
+def query(name: str, *args):
+    """Call an entry point that returns a value rather than a status."""
+    return getattr(load_library(), name)(*args)
+
+
+def stream_handle(device: torch.device) -> int:
+    """hipStream_t of torch's current stream on `device`."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return DTYPE_CODES[dtype]
+    except KeyError:
+        raise RuntimeError(f"unsupported dtype {dtype}; expected bfloat16 or float16") from None

@@ -1,0 +1,795 @@
+"""Attention backend lifecycle, registry and the MI355X (gfx950) backend.
+
+The first half restates the reference's backend-neutral contract
+(nanovllm/layers/attention_backend.py): ``AttentionRoute`` (:112-117),
+``AttentionPlan`` (:120-135), the ``AttentionBackend`` lifecycle (:174-275),
+``AttentionBackendRegistry`` (:1228-1381), metadata validation (:1384-1481),
+batch classification (:1484-1491) and the cacheless warmup fallback
+(:1556-1624).
+
+The second half is the new backend.  ``MI355XAttentionBackendMixin`` holds the
+whole implementation and takes the plan/route/batch-type classes from class
+attributes, so the same code can subclass either this module's
+``AttentionBackend`` (``MI355XAttentionBackend`` below) or the reference's own
+``AttentionBackend`` and be registered in the reference's registry unchanged.
+
+Per step: ``build_metadata`` turns the trusted host ints of
+``CommonAttentionMetadata`` into device work lists (no device reads),
+``build_plan`` classifies the batch once and picks one route, and ``forward``
+launches the gfx950 kernels on the current stream into a reusable,
+backend-owned output buffer:
+
+* DECODE        -> paged GQA decode (split-K + in-launch LSE merge)
+* PREFILL       -> ragged causal chunked prefill over prefix-cached pages
+* MIXED_UNIFIED -> one launch writing ``out[:P]`` (prefill) and ``out[P:]`` (decode)
+* MIXED_SPLIT   -> prefill launch into ``out[:P]`` + decode launch into ``out[P:]``
+* WARMUP        -> cacheless causal attention (no pages; one-time memory probe)
+"""
+
+from __future__ import annotations
+
+import os
+from dataclasses import dataclass
+from enum import Enum
+from math import sqrt
+from types import MappingProxyType
+from typing import Any
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import _native, ops
+from .context import BatchType, CommonAttentionMetadata
+
+
+class AttentionRoute(str, Enum):
+    WARMUP = "warmup"
+    PREFILL = "prefill"
+    DECODE = "decode"
+    MIXED_UNIFIED = "mixed_unified"
+    MIXED_SPLIT = "mixed_split"
+
+
+@dataclass(frozen=True)
+class AttentionPlan:
+    """One explicit, backend-owned execution decision for a scheduled batch."""
+
+    batch_type: BatchType
+    route: AttentionRoute
+    common: CommonAttentionMetadata
+    metadata: Any
+
+    @property
+    def common_metadata(self) -> CommonAttentionMetadata:
+        return self.common
+
+    @property
+    def backend_metadata(self) -> Any:
+        return self.metadata
+
+
+class AttentionBackend:
+    """Unified lifecycle implemented by every complete attention backend."""
+
+    backend_name = "base"
+    supports_full_decode_graph = False
+
+    def __init__(
+        self,
+        num_q_heads: int,
+        num_kv_heads: int,
+        head_dim: int,
+        block_size: int,
+        dtype: torch.dtype,
+    ) -> None:
+        if num_q_heads <= 0 or num_kv_heads <= 0:
+            raise ValueError("attention head counts must be positive")
+        if num_q_heads % num_kv_heads:
+            raise ValueError("num_q_heads must be divisible by num_kv_heads")
+        if head_dim <= 0 or block_size <= 0:
+            raise ValueError("head_dim and block_size must be positive")
+        self.num_q_heads = num_q_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.block_size = block_size
+        self.dtype = dtype
+        self.softmax_scale = 1.0 / sqrt(head_dim)
+
+    @classmethod
+    def support_reason(cls, *, block_size: int, dtype: torch.dtype, device=None, **_: Any) -> str | None:
+        del block_size, dtype, device
+        return None
+
+    @classmethod
+    def supports(cls, **capabilities: Any) -> bool:
+        return cls.support_reason(**capabilities) is None
+
+    def build_metadata(self, common: CommonAttentionMetadata) -> Any:
+        raise NotImplementedError
+
+    def build_plan(self, common: CommonAttentionMetadata, metadata: Any | None = None) -> AttentionPlan:
+        raise NotImplementedError
+
+    def forward(self, q, k, v, k_cache, v_cache, plan: AttentionPlan) -> torch.Tensor:
+        raise NotImplementedError
+
+    def create_full_decode_graph_state(self, batch_size: int, page_indices_capacity: int, device) -> Any:
+        raise RuntimeError(f"{type(self).__name__} does not support full decode CUDA Graph")
+
+    def full_decode_graph_metadata_fits(self, state: Any, plan: AttentionPlan) -> bool:
+        del state, plan
+        return False
+
+    def plan_full_decode_graph(self, state: Any, plan: AttentionPlan) -> None:
+        raise RuntimeError(f"{type(self).__name__} does not support full decode CUDA Graph")
+
+    def activate_full_decode_graph(self, state: Any) -> None:
+        raise RuntimeError(f"{type(self).__name__} does not support full decode CUDA Graph")
+
+    def deactivate_full_decode_graph(self) -> None:
+        return None
+
+
+# --------------------------------------------------------------------------
+# Shared validation helpers (nanovllm/layers/attention_backend.py:1384-1553).
+# --------------------------------------------------------------------------
+
+def _validate_common_metadata(common: Any, *, require_cuda: bool, common_type=CommonAttentionMetadata) -> None:
+    if not isinstance(common, common_type):
+        raise TypeError("common must be CommonAttentionMetadata")
+    for name in (
+        "num_prefill_seqs",
+        "num_decode_seqs",
+        "num_prefill_tokens",
+        "num_decode_tokens",
+        "max_q_len",
+        "max_kv_len",
+        "num_kv_blocks",
+        "num_prefill_kv_blocks",
+    ):
+        value = getattr(common, name)
+        if isinstance(value, bool) or not isinstance(value, int):
+            raise TypeError(f"common.{name} must be an int")
+        if value < 0:
+            raise ValueError(f"common.{name} must be non-negative")
+    if common.num_seqs <= 0:
+        raise ValueError("attention metadata must contain at least one sequence")
+    if common.num_decode_tokens != common.num_decode_seqs:
+        raise ValueError("decode suffix must contain one query token per sequence")
+    if not isinstance(common.trusted, bool):
+        raise TypeError("common.trusted must be a bool")
+    for name in ("query_start_loc", "seq_lens", "slot_mapping"):
+        tensor = getattr(common, name)
+        if not isinstance(tensor, torch.Tensor):
+            raise TypeError(f"common.{name} must be a torch.Tensor")
+        if tensor.dtype != torch.int32:
+            raise TypeError(f"common.{name} must have dtype torch.int32")
+        if tensor.ndim != 1:
+            raise ValueError(f"common.{name} must be one-dimensional")
+        if require_cuda and tensor.device.type != "cuda":
+            raise ValueError(f"common.{name} must be on CUDA")
+    if common.query_start_loc.numel() != common.num_seqs + 1:
+        raise ValueError("query_start_loc length must equal number of sequences + 1")
+    if common.seq_lens.numel() != common.num_seqs:
+        raise ValueError("seq_lens length must equal number of sequences")
+    if common.slot_mapping.numel() != common.num_query_tokens:
+        raise ValueError("slot_mapping length must equal number of query tokens")
+    if not common.trusted:
+        if int(common.query_start_loc[0].item()) != 0:
+            raise ValueError("query_start_loc must start at zero")
+        if int(common.query_start_loc[-1].item()) != common.num_query_tokens:
+            raise ValueError("query_start_loc must end at num_query_tokens")
+        query_lengths = common.query_start_loc[1:] - common.query_start_loc[:-1]
+        if common.num_decode_seqs and not bool(torch.all(query_lengths[common.num_prefill_seqs:] == 1).item()):
+            raise ValueError("every decode sequence must have one query token")
+        if not bool(torch.all(common.seq_lens > 0).item()):
+            raise ValueError("all KV sequence lengths must be positive")
+    block_tables = common.block_tables
+    if block_tables is not None:
+        if not isinstance(block_tables, torch.Tensor):
+            raise TypeError("common.block_tables must be a torch.Tensor")
+        if block_tables.dtype != torch.int32:
+            raise TypeError("common.block_tables must have dtype torch.int32")
+        if block_tables.ndim != 2:
+            raise ValueError("common.block_tables must be two-dimensional")
+        if block_tables.size(0) != common.num_seqs:
+            raise ValueError("block_tables row count must equal number of sequences")
+        if require_cuda and block_tables.device.type != "cuda":
+            raise ValueError("common.block_tables must be on CUDA")
+
+
+def _classify_batch(common: Any, batch_type_enum=BatchType):
+    if common.num_prefill_seqs == 0:
+        if common.num_decode_seqs <= 0:
+            raise ValueError("pure decode batch must contain decode requests")
+        return batch_type_enum.PURE_DECODE
+    if common.num_decode_seqs == 0:
+        return batch_type_enum.PURE_PREFILL
+    return batch_type_enum.MIXED
+
+
+def _require_plan_metadata(plan: Any, metadata_type: type, backend_name: str, plan_type=AttentionPlan):
+    if not isinstance(plan, plan_type):
+        raise TypeError("attention forward requires AttentionPlan")
+    if not isinstance(plan.metadata, metadata_type):
+        raise TypeError(f"{backend_name} plan carries incompatible backend metadata")
+    return plan.metadata
+
+
+def _has_cache(cache: torch.Tensor | None) -> bool:
+    return isinstance(cache, torch.Tensor) and cache.numel() > 0
+
+
+def _torch_sdpa_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, common: Any) -> torch.Tensor:
+    """Cacheless causal varlen attention, one SDPA call per sequence.
+
+    Restates the reference's dependency-free warmup path
+    (nanovllm/layers/attention_backend.py:1580-1624).  Operands are made
+    contiguous before SDPA so no batched product sees a transposed bf16 view.
+    """
+    if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
+        raise ValueError("cacheless attention expects rank-3 Q/K/V")
+    if k.shape != v.shape:
+        raise ValueError("cacheless key and value shapes must match")
+    if q.size(0) != k.size(0):
+        raise ValueError("cacheless warmup requires matching query and KV token counts")
+    if q.size(1) % k.size(1):
+        raise ValueError("query head count must be divisible by KV head count")
+    starts = common.query_start_loc
+    boundaries = starts.cpu().tolist()
+    kv_repeat = q.size(1) // k.size(1)
+    outputs = []
+    for start, end in zip(boundaries[:-1], boundaries[1:]):
+        q_seq = q[start:end].transpose(0, 1).unsqueeze(0).contiguous()
+        k_seq = k[start:end].transpose(0, 1).unsqueeze(0)
+        v_seq = v[start:end].transpose(0, 1).unsqueeze(0)
+        if kv_repeat != 1:
+            k_seq = k_seq.repeat_interleave(kv_repeat, dim=1)
+            v_seq = v_seq.repeat_interleave(kv_repeat, dim=1)
+        output = F.scaled_dot_product_attention(
+            q_seq, k_seq.contiguous(), v_seq.contiguous(), is_causal=True, scale=1.0 / sqrt(q.size(-1))
+        )
+        outputs.append(output.squeeze(0).transpose(0, 1))
+    return torch.cat(outputs, dim=0) if outputs else torch.empty_like(q)
+
+
+# --------------------------------------------------------------------------
+# MI355X backend.
+# --------------------------------------------------------------------------
+
+HEAD_DIM = ops.HEAD_DIM
+PAGE_SIZE = ops.PAGE_SIZE
+MAX_GROUP = 16
+
+
+@dataclass(frozen=True)
+class MI355XAttentionMetadata:
+    """Backend-private per-step metadata: device work lists built on the host.
+
+    ``decode_items`` is int32 ``[num_decode_items, 8]`` (see
+    ``make_decode_items``); ``None`` when the batch has no decode sequences.
+    ``kv_indptr`` is the page CSR offset list (host ints): sequence ``s`` owns
+    pages ``block_tables[s, :kv_indptr[s+1]-kv_indptr[s]]``.
+    """
+
+    query_start_loc: torch.Tensor
+    seq_lens: torch.Tensor
+    block_tables: torch.Tensor | None
+    kv_indptr: tuple[int, ...]
+    num_pages: int
+    num_prefill_pages: int
+    decode_items: torch.Tensor | None = None
+    num_decode_items: int = 0
+    num_decode_part_slots: int = 0
+    decode_chunk_pages: int = 0
+
+    @property
+    def is_cacheless(self) -> bool:
+        return self.block_tables is None
+
+
+def choose_decode_chunk_pages(total_pages: int, num_kv_heads: int) -> int:
+    """Pages per decode work item.
+
+    Short batches are cut fine so that enough wavefronts stream at once
+    (256 CUs x 8 resident decode waves); long contexts use long chunks to keep
+    the split-K partial traffic small.  Always even and within [8, 128].
+    ``MVA_DECODE_CHUNK_PAGES`` overrides the choice.
+    """
+    override = os.environ.get("MVA_DECODE_CHUNK_PAGES")
+    if override:
+        pages = int(override)
+    else:
+        target_items = 8192
+        pages = -(-total_pages * num_kv_heads // target_items)
+    pages = max(8, min(ops.MAX_CHUNK_PAGES, pages))
+    return pages + (pages & 1)
+
+
+def make_decode_items(
+    block_counts: np.ndarray | tuple[int, ...],
+    first_seq: int,
+    first_q_row: int,
+    chunk_pages: int,
+) -> tuple[np.ndarray, int]:
+    """Decode work items for sequences ``first_seq + i`` with ``block_counts[i]`` pages.
+
+    Each item is ``(seq, page_begin, page_end, chunk, n_chunks, part_base,
+    q_row, 0)``; sequence ``first_seq + i`` reads query row ``first_q_row + i``.
+    Items are ordered longest first.  Returns ``(items, num_part_slots)``.
+    """
+    counts = np.asarray(block_counts, dtype=np.int64)
+    if counts.size == 0:
+        return np.zeros((0, ops.DECODE_ITEM_INTS), dtype=np.int32), 0
+    nchunks = (counts + chunk_pages - 1) // chunk_pages
+    nchunks = np.maximum(nchunks, 1)
+    total = int(nchunks.sum())
+    seq_local = np.repeat(np.arange(counts.size), nchunks)
+    first_item = np.cumsum(nchunks) - nchunks
+    chunk = np.arange(total) - np.repeat(first_item, nchunks)
+    begin = chunk * chunk_pages
+    end = np.minimum(begin + chunk_pages, np.repeat(counts, nchunks))
+    split = nchunks > 1
+    split_sizes = np.where(split, nchunks, 0)
+    part_base_seq = np.cumsum(split_sizes) - split_sizes
+    items = np.zeros((total, ops.DECODE_ITEM_INTS), dtype=np.int32)
+    items[:, 0] = first_seq + seq_local
+    items[:, 1] = begin
+    items[:, 2] = end
+    items[:, 3] = chunk
+    items[:, 4] = np.repeat(nchunks, nchunks)
+    items[:, 5] = np.repeat(part_base_seq, nchunks)
+    items[:, 6] = first_q_row + seq_local
+    order = np.argsort(-(end - begin), kind="stable")
+    return items[order], int(split_sizes.sum())
+
+
+def _to_device(array: np.ndarray, device: torch.device) -> torch.Tensor:
+    """Host int32 array -> device tensor through pinned memory (async H2D)."""
+    host = torch.from_numpy(np.ascontiguousarray(array))
+    if device.type != "cuda":
+        return host.to(device)
+    return host.pin_memory().to(device, non_blocking=True)
+
+
+def _device_arch(device: torch.device) -> str:
+    props = torch.cuda.get_device_properties(device)
+    return getattr(props, "gcnArchName", "") or ""
+
+
+class MI355XAttentionBackendMixin:
+    """The MI355X backend implementation, independent of the concrete base class.
+
+    Subclasses combine it with an ``AttentionBackend`` base and name the
+    plan/route/batch-type/metadata classes of that base's family.
+    """
+
+    backend_name = "mi355x"
+    supports_full_decode_graph = False
+    default_attention_mode = "unified"
+    plan_type: type = AttentionPlan
+    route_type: type = AttentionRoute
+    batch_type_enum: type = BatchType
+    common_type: type = CommonAttentionMetadata
+
+    def __init__(
+        self,
+        num_q_heads: int,
+        num_kv_heads: int,
+        head_dim: int,
+        block_size: int,
+        dtype: torch.dtype,
+        attention_mode: str | None = None,
+    ) -> None:
+        super().__init__(num_q_heads, num_kv_heads, head_dim, block_size, dtype)
+        attention_mode = attention_mode or self.default_attention_mode
+        if attention_mode not in ("unified", "split"):
+            raise ValueError("attention_mode must be 'unified' or 'split'")
+        if dtype not in (torch.float16, torch.bfloat16):
+            raise TypeError("MI355X attention supports only float16 and bfloat16")
+        if head_dim != HEAD_DIM:
+            raise ValueError(f"MI355X attention requires head_dim {HEAD_DIM}")
+        if block_size != PAGE_SIZE:
+            raise ValueError(f"MI355X attention requires block_size {PAGE_SIZE}")
+        if num_q_heads // num_kv_heads > MAX_GROUP:
+            raise ValueError(f"MI355X attention supports at most {MAX_GROUP} query heads per KV head")
+        _native.load_library()
+        self.attention_mode = attention_mode
+        self._reset_state()
+
+    def _reset_state(self) -> None:
+        self._planned_route: str | None = None
+        self._route_counts = {route.value: 0 for route in self.route_type}
+        self._output_buffer: torch.Tensor | None = None
+        self._workspace: torch.Tensor | None = None
+
+    # ---- capability contract -------------------------------------------------
+    @classmethod
+    def support_reason(
+        cls,
+        *,
+        block_size: int,
+        dtype: torch.dtype,
+        device: torch.device | str | None = None,
+        num_q_heads: int | None = None,
+        num_kv_heads: int | None = None,
+        head_dim: int | None = None,
+        attention_mode: str = "unified",
+        **_: Any,
+    ) -> str | None:
+        if block_size != PAGE_SIZE:
+            return f"block_size must be {PAGE_SIZE}"
+        if head_dim is not None and head_dim != HEAD_DIM:
+            return f"head_dim must be {HEAD_DIM}"
+        if dtype not in (torch.float16, torch.bfloat16):
+            return "dtype must be float16 or bfloat16"
+        if attention_mode not in ("unified", "split"):
+            return "attention_mode must be 'unified' or 'split'"
+        if num_q_heads is not None and num_kv_heads is not None:
+            if num_kv_heads <= 0 or num_q_heads % num_kv_heads:
+                return "num_q_heads must be a multiple of num_kv_heads"
+            if num_q_heads // num_kv_heads > MAX_GROUP:
+                return f"at most {MAX_GROUP} query heads per KV head"
+        selected = (
+            torch.device(device)
+            if device is not None
+            else torch.device("cuda", torch.cuda.current_device() if torch.cuda.is_available() else 0)
+        )
+        if selected.type != "cuda" or not torch.cuda.is_available():
+            return "a ROCm GPU device is required"
+        arch = _device_arch(selected)
+        if not arch.startswith("gfx950"):
+            return f"a gfx950 (MI355X) device is required, found {arch or 'unknown'}"
+        if not _native.native_available():
+            return f"native library unavailable ({_native.LIB_PATH}); run `python -m my_vllm_amd.build`"
+        return None
+
+    @property
+    def planned_route(self) -> str | None:
+        return self._planned_route
+
+    @property
+    def route_counts(self):
+        return MappingProxyType(dict(self._route_counts))
+
+    # ---- per-step metadata and plan ------------------------------------------
+    def build_metadata(self, common) -> MI355XAttentionMetadata:
+        _validate_common_metadata(common, require_cuda=True, common_type=self.common_type)
+        if common.block_tables is None:
+            return MI355XAttentionMetadata(
+                query_start_loc=common.query_start_loc,
+                seq_lens=common.seq_lens,
+                block_tables=None,
+                kv_indptr=(),
+                num_pages=0,
+                num_prefill_pages=0,
+            )
+        block_tables = common.block_tables
+        max_pages = block_tables.size(1)
+        if common.trusted:
+            block_counts = common.block_counts
+            if not isinstance(block_counts, tuple):
+                raise TypeError("trusted block_counts must be a tuple")
+            if len(block_counts) != common.num_seqs:
+                raise ValueError("trusted block_counts length must equal num_seqs")
+            if any(
+                isinstance(count, bool) or not isinstance(count, int) or not 0 < count <= max_pages
+                for count in block_counts
+            ):
+                raise ValueError("trusted block_counts contains an invalid row count")
+            counts = np.asarray(block_counts, dtype=np.int64)
+        else:
+            page_counts = (common.seq_lens.to(torch.int64) + self.block_size - 1) // self.block_size
+            counts = page_counts.cpu().numpy()
+            if np.any(counts <= 0) or np.any(counts > max_pages):
+                raise ValueError("seq_lens need more pages than block_tables holds")
+            columns = torch.arange(max_pages, device=block_tables.device)
+            needed = columns.unsqueeze(0) < page_counts.to(block_tables.device).unsqueeze(1)
+            if bool(torch.any(block_tables[needed] < 0).item()):
+                raise ValueError("block_tables contains an invalid page index")
+        offsets = np.concatenate(([0], np.cumsum(counts)))
+        num_pages = int(offsets[-1])
+        num_prefill_pages = int(offsets[common.num_prefill_seqs])
+        if common.trusted:
+            if common.num_kv_blocks != num_pages:
+                raise ValueError("trusted num_kv_blocks must match block_counts")
+            if common.num_prefill_kv_blocks != num_prefill_pages:
+                raise ValueError("trusted num_prefill_kv_blocks must match block_counts")
+
+        decode_items = None
+        num_decode_items = 0
+        num_part_slots = 0
+        chunk_pages = 0
+        if common.num_decode_seqs:
+            decode_counts = counts[common.num_prefill_seqs:]
+            chunk_pages = choose_decode_chunk_pages(int(decode_counts.sum()), self.num_kv_heads)
+            items, num_part_slots = make_decode_items(
+                decode_counts, common.num_prefill_seqs, common.num_prefill_tokens, chunk_pages
+            )
+            num_decode_items = items.shape[0]
+            decode_items = _to_device(items, block_tables.device)
+        return MI355XAttentionMetadata(
+            query_start_loc=common.query_start_loc,
+            seq_lens=common.seq_lens,
+            block_tables=block_tables,
+            kv_indptr=tuple(int(x) for x in offsets),
+            num_pages=num_pages,
+            num_prefill_pages=num_prefill_pages,
+            decode_items=decode_items,
+            num_decode_items=num_decode_items,
+            num_decode_part_slots=num_part_slots,
+            decode_chunk_pages=chunk_pages,
+        )
+
+    def build_plan(self, common, metadata: MI355XAttentionMetadata | None = None):
+        if metadata is None:
+            metadata = self.build_metadata(common)
+        if not isinstance(metadata, MI355XAttentionMetadata):
+            raise TypeError("MI355X attention requires MI355XAttentionMetadata")
+        Route = self.route_type
+        Batch = self.batch_type_enum
+        # The single phase classification point for the whole batch.
+        batch_type = _classify_batch(common, Batch)
+        if metadata.is_cacheless:
+            route = Route.WARMUP
+        elif batch_type is Batch.PURE_PREFILL:
+            route = Route.PREFILL
+        elif batch_type is Batch.PURE_DECODE:
+            route = Route.DECODE
+        elif self.attention_mode == "unified":
+            route = Route.MIXED_UNIFIED
+        else:
+            route = Route.MIXED_SPLIT
+        plan = self.plan_type(batch_type, route, common, metadata)
+        self._planned_route = route.value
+        self._route_counts[route.value] += 1
+        return plan
+
+    # ---- buffers ---------------------------------------------------------------
+    def _get_reusable_attention_output(self, q: torch.Tensor) -> torch.Tensor:
+        required = q.size(0)
+        buffer = self._output_buffer
+        if (
+            buffer is None
+            or buffer.size(0) < required
+            or buffer.shape[1:] != q.shape[1:]
+            or buffer.device != q.device
+            or buffer.dtype != q.dtype
+        ):
+            buffer = torch.empty_like(q)
+            self._output_buffer = buffer
+        return buffer[:required]
+
+    def _get_workspace(self, nbytes: int, device: torch.device) -> torch.Tensor | None:
+        if nbytes <= 0:
+            return None
+        ws = self._workspace
+        if ws is None or ws.numel() < nbytes or ws.device != device:
+            # Zeroed once: the kernels leave their counters at zero on exit.
+            ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            self._workspace = ws
+        return ws
+
+    # ---- forward ------------------------------------------------------------------
+    def _validate_inputs(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
+        if q.device.type != "cuda" or q.dtype != self.dtype:
+            raise ValueError("query must be a CUDA tensor with the backend dtype")
+        if q.ndim != 3 or q.shape[1:] != (self.num_q_heads, self.head_dim):
+            raise ValueError("query must have shape [tokens, num_q_heads, head_dim]")
+        if q.stride(2) != 1:
+            raise ValueError("query must have unit stride in head_dim")
+        expected_tail = (self.block_size, self.num_kv_heads, self.head_dim)
+        for name, cache in (("key", k_cache), ("value", v_cache)):
+            if cache.device != q.device or cache.dtype != self.dtype:
+                raise ValueError(f"{name} cache must share the query device and dtype")
+            if cache.ndim != 4 or cache.shape[1:] != expected_tail:
+                raise ValueError(f"{name} cache must have shape [pages, block_size, num_kv_heads, head_dim]")
+            if cache.stride(3) != 1 or cache.stride(2) != self.head_dim or cache.stride(1) != self.num_kv_heads * self.head_dim:
+                raise ValueError(f"{name} cache pages must be contiguous")
+        if k_cache.shape != v_cache.shape or k_cache.stride() != v_cache.stride():
+            raise ValueError("key and value caches must share shape and layout")
+
+    def forward(self, q, k, v, k_cache, v_cache, plan) -> torch.Tensor:
+        metadata = _require_plan_metadata(plan, MI355XAttentionMetadata, self.backend_name, self.plan_type)
+        Route = self.route_type
+        Batch = self.batch_type_enum
+        has_k_cache = _has_cache(k_cache)
+        has_v_cache = _has_cache(v_cache)
+        if has_k_cache != has_v_cache:
+            raise ValueError("key and value caches must both be present or absent")
+        route = plan.route
+        if route is Route.WARMUP:
+            if has_k_cache:
+                raise ValueError("MI355X warmup route requires an empty KV cache")
+            if not metadata.is_cacheless:
+                raise ValueError("MI355X warmup route requires cacheless metadata")
+            output = _torch_sdpa_varlen(q, k, v, plan.common)
+            scratch = self._get_reusable_attention_output(q)
+            scratch.copy_(output)
+            return scratch
+
+        expected = {
+            Route.PREFILL: Batch.PURE_PREFILL,
+            Route.DECODE: Batch.PURE_DECODE,
+            Route.MIXED_UNIFIED: Batch.MIXED,
+            Route.MIXED_SPLIT: Batch.MIXED,
+        }.get(route)
+        if expected is None:
+            raise RuntimeError(f"invalid planned MI355X route: {route!r}")
+        if plan.batch_type is not expected:
+            raise ValueError("MI355X route does not match the planned BatchType")
+        if not has_k_cache:
+            raise ValueError("paged MI355X route requires an allocated KV cache")
+        if metadata.is_cacheless:
+            raise ValueError("paged MI355X route requires page metadata")
+        self._validate_inputs(q, k_cache, v_cache)
+        common = plan.common
+        if q.size(0) != common.num_query_tokens:
+            raise ValueError("query token count does not match the attention plan")
+
+        output = self._get_reusable_attention_output(q)
+        if route is Route.DECODE:
+            self._run_decode(q, k_cache, v_cache, common, metadata, output)
+            return output
+        if route is Route.PREFILL:
+            self._run_prefill(q, k_cache, v_cache, common, metadata, output)
+            return output
+        if route is Route.MIXED_SPLIT:
+            if common.num_prefill_seqs:
+                self._run_prefill(q, k_cache, v_cache, common, metadata, output)
+            if common.num_decode_seqs:
+                self._run_decode(q, k_cache, v_cache, common, metadata, output)
+            return output
+        self._run_mixed(q, k_cache, v_cache, common, metadata, output)
+        return output
+
+    def _run_decode(self, q, k_cache, v_cache, common, metadata: MI355XAttentionMetadata, output) -> None:
+        group = self.num_q_heads // self.num_kv_heads
+        ws_bytes = ops.decode_workspace_bytes(
+            common.num_seqs, metadata.num_decode_part_slots, self.num_kv_heads, group
+        )
+        workspace = self._get_workspace(ws_bytes, q.device)
+        ops.paged_decode(
+            q,
+            k_cache,
+            v_cache,
+            metadata.block_tables,
+            metadata.seq_lens,
+            metadata.decode_items,
+            metadata.num_decode_items,
+            common.num_seqs,
+            metadata.num_decode_part_slots,
+            output,
+            workspace,
+            self.softmax_scale,
+        )
+
+    def _run_prefill(self, q, k_cache, v_cache, common, metadata, output) -> None:
+        raise NotImplementedError("MI355X prefill kernel is not built yet")
+
+    def _run_mixed(self, q, k_cache, v_cache, common, metadata, output) -> None:
+        raise NotImplementedError("MI355X mixed kernel is not built yet")
+
+
+class MI355XAttentionBackend(MI355XAttentionBackendMixin, AttentionBackend):
+    """gfx950 backend registered as ``"mi355x"`` (MIXED batches: one launch)."""
+
+
+class MI355XSplitAttentionBackend(MI355XAttentionBackend):
+    """Same kernels; MIXED batches run as prefill + decode launches ("mi355x_split")."""
+
+    backend_name = "mi355x_split"
+    default_attention_mode = "split"
+
+
+class AttentionBackendRegistry:
+    """Registry of complete attention backends (reference :1228-1381 semantics).
+
+    ``create("auto", ...)`` selects the MI355X backend when it supports the
+    requested capabilities.  Unlike the reference, ``attention_mode`` is passed
+    to every registered backend whose constructor accepts it.
+    """
+
+    _BACKENDS: dict[str, type[AttentionBackend]] = {
+        "mi355x": MI355XAttentionBackend,
+        "mi355x_split": MI355XSplitAttentionBackend,
+    }
+    _ALIASES: dict[str, str] = {"hip": "mi355x", "gfx950": "mi355x"}
+
+    @classmethod
+    def registered_names(cls) -> tuple[str, ...]:
+        return tuple(cls._BACKENDS)
+
+    @classmethod
+    def names(cls) -> tuple[str, ...]:
+        return cls.registered_names()
+
+    @classmethod
+    def register(cls, name: str, backend_type: type[AttentionBackend]) -> None:
+        if not isinstance(name, str):
+            raise TypeError("attention backend name must be a string")
+        normalized = name.strip().lower()
+        if not normalized or normalized == "auto":
+            raise ValueError("attention backend name must be non-empty and not 'auto'")
+        if normalized in cls._BACKENDS or normalized in cls._ALIASES:
+            raise ValueError(f"attention backend name {normalized!r} is already registered")
+        if not isinstance(backend_type, type) or not issubclass(backend_type, AttentionBackend):
+            raise TypeError("backend_type must be an AttentionBackend subclass")
+        cls._BACKENDS[normalized] = backend_type
+
+    @staticmethod
+    def _support_status(backend_type: type[AttentionBackend], capabilities: dict[str, Any]):
+        supported = backend_type.supports(**capabilities)
+        if type(supported) is not bool:
+            raise TypeError(f"{backend_type.__name__}.supports() must return a bool")
+        if supported:
+            return True, None
+        reason = backend_type.support_reason(**capabilities)
+        if reason is not None and not isinstance(reason, str):
+            raise TypeError(f"{backend_type.__name__}.support_reason() must return a string or None")
+        return False, reason or "supports() returned False"
+
+    @classmethod
+    def create(
+        cls,
+        name: str = "auto",
+        *,
+        num_q_heads: int,
+        num_kv_heads: int,
+        head_dim: int,
+        block_size: int,
+        dtype: torch.dtype,
+        attention_mode: str = "unified",
+        device: torch.device | str | None = None,
+    ) -> AttentionBackend:
+        if not isinstance(name, str):
+            raise TypeError("attention backend name must be a string")
+        requested = name.strip().lower()
+        canonical = cls._ALIASES.get(requested, requested)
+        capabilities = {
+            "num_q_heads": num_q_heads,
+            "num_kv_heads": num_kv_heads,
+            "head_dim": head_dim,
+            "block_size": block_size,
+            "dtype": dtype,
+            "device": device,
+            "attention_mode": attention_mode,
+        }
+        init_kwargs = {
+            "num_q_heads": num_q_heads,
+            "num_kv_heads": num_kv_heads,
+            "head_dim": head_dim,
+            "block_size": block_size,
+            "dtype": dtype,
+        }
+        if canonical == "auto":
+            supported, reason = cls._support_status(MI355XAttentionBackend, capabilities)
+            if supported:
+                return MI355XAttentionBackend(**init_kwargs, attention_mode=attention_mode)
+            raise RuntimeError(f"No usable attention backend. mi355x: {reason}")
+        backend_type = cls._BACKENDS.get(canonical)
+        if backend_type is None:
+            supported_names = ", ".join(("auto", *cls.registered_names()))
+            raise ValueError(f"unknown attention backend {name!r}; choose from {supported_names}")
+        supported, reason = cls._support_status(backend_type, capabilities)
+        if not supported:
+            raise RuntimeError(f"{canonical} attention backend is unusable: {reason}")
+        if issubclass(backend_type, MI355XAttentionBackendMixin):
+            mode = "split" if backend_type.default_attention_mode == "split" else attention_mode
+            return backend_type(**init_kwargs, attention_mode=mode)
+        return backend_type(**init_kwargs)
+
+
+__all__ = [
+    "AttentionBackend",
+    "AttentionBackendRegistry",
+    "AttentionPlan",
+    "AttentionRoute",
+    "MI355XAttentionBackend",
+    "MI355XAttentionBackendMixin",
+    "MI355XAttentionMetadata",
+    "MI355XSplitAttentionBackend",
+    "choose_decode_chunk_pages",
+    "make_decode_items",
+]

@@ -1,0 +1,79 @@
+// Shared device helpers for the gfx950 (MI355X, CDNA4) kernels of this library.
+//
+// Everything here is written for one target: 64-lane wavefronts, bf16/fp16
+// MFMA through the gfx950 builtins, and 16-byte global/LDS accesses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace mva {
+
+// Element codes shared with the host side (include/my_vllm_amd.h).
+enum DType : int { kBF16 = 0, kF16 = 1 };
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Per-element-type traits: the 8-wide vector used as an MFMA operand and the
+// matching gfx950 MFMA instructions (fp32 accumulate).
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<__bf16> {
+  typedef bf16x8 v8;
+  typedef bf16x4 v4;
+  __device__ static inline f32x4 mfma16(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ static inline f32x16 mfma32(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Elem<_Float16> {
+  typedef f16x8 v8;
+  typedef f16x4 v4;
+  __device__ static inline f32x4 mfma16(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static inline f32x16 mfma32(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// 16-byte load/store of an 8-element vector; callers guarantee alignment.
+template <typename V>
+__device__ inline V ld16(const void* p) {
+  return *reinterpret_cast<const V*>(p);
+}
+template <typename V>
+__device__ inline void st16(void* p, V v) {
+  *reinterpret_cast<V*>(p) = v;
+}
+
+// Compiler-level ordering point for LDS traffic that is shared between lanes
+// of one wavefront.  LDS instructions of a wavefront execute in issue order,
+// so only the compiler has to be kept from reordering them.
+__device__ inline void wave_lds_fence() {
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ inline float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+__device__ inline float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+}  // namespace mva

@@ -1,0 +1,159 @@
+"""Validated Python entry points over the gfx950 C ABI.
+
+Each function checks shapes, dtypes, devices and layout on the host, with the
+reference's exception classes and messages, then launches the kernel on
+torch's current stream.  None of them synchronizes or reads device memory.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native
+
+HEAD_DIM = 128
+PAGE_SIZE = 16
+# int32 fields per decode work item (kDecodeItemInts in csrc/paged_decode.h).
+DECODE_ITEM_INTS = 8
+# Longest chunk one decode work item may cover (kMaxChunkPages).
+MAX_CHUNK_PAGES = 128
+
+
+def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
+    """``silu(x[..., :I]) * x[..., I:]`` into a new contiguous ``[..., I]`` tensor.
+
+    Argument checks and messages follow the reference's compiled op
+    (csrc/silu_and_mul.cpp:8-18); an empty input gives an empty output
+    (csrc/silu_and_mul_kernel.cu:61-63).
+    """
+    if not x.is_cuda:
+        raise RuntimeError("silu_and_mul expects a CUDA tensor")
+    if not x.is_contiguous():
+        raise RuntimeError("silu_and_mul expects a contiguous tensor")
+    if x.dim() < 1:
+        raise RuntimeError("silu_and_mul expects at least one dimension")
+    if x.dtype not in _native.DTYPE_CODES:
+        raise RuntimeError("silu_and_mul only supports float16 and bfloat16")
+    width = x.size(-1)
+    if width <= 0 or width % 2:
+        raise RuntimeError(
+            "silu_and_mul expects the last dimension to be a positive even number"
+        )
+    hidden = width // 2
+    out = torch.empty((*x.shape[:-1], hidden), dtype=x.dtype, device=x.device)
+    if out.numel() == 0:
+        return out
+    rows = x.numel() // width
+    _native.call(
+        "mva_silu_and_mul",
+        x.data_ptr(),
+        out.data_ptr(),
+        rows,
+        hidden,
+        _native.dtype_code(x.dtype),
+        _native.stream_handle(x.device),
+    )
+    return out
+
+
+def store_kvcache(
+    key: torch.Tensor,
+    value: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+) -> None:
+    """Scatter K/V rows into the paged cache by ``slot_mapping`` (``< 0`` = skip).
+
+    Layout contract of the reference's store (nanovllm/layers/attention.py:34-41):
+    ``key``/``value`` are ``[N, Hkv, D]`` with unit element stride and head
+    stride ``D`` (the token stride is free: V is a view into a packed qkv
+    projection); the caches are contiguous ``[P, page, Hkv, D]``.
+    """
+    if key.dim() != 3 or value.shape != key.shape:
+        raise ValueError("key and value must both have shape [tokens, num_kv_heads, head_dim]")
+    num_tokens, num_heads, head_dim = key.shape
+    row_elems = num_heads * head_dim
+    if slot_mapping.numel() != num_tokens:
+        raise ValueError("slot_mapping must contain one slot per token")
+    if slot_mapping.dtype not in (torch.int32, torch.int64):
+        raise TypeError("slot_mapping must be int32 or int64")
+    if key.stride(-1) != 1 or value.stride(-1) != 1:
+        raise ValueError("key/value must have unit stride in the head dimension")
+    if key.stride(1) != head_dim or value.stride(1) != head_dim:
+        raise ValueError("key/value heads must be packed (stride(1) == head_dim)")
+    for name, cache in (("k_cache", k_cache), ("v_cache", v_cache)):
+        if not cache.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+        if cache.dtype != key.dtype:
+            raise TypeError(f"{name} dtype {cache.dtype} does not match key dtype {key.dtype}")
+        if cache.numel() % row_elems or (cache.dim() >= 2 and cache.stride(1) != row_elems):
+            raise ValueError(f"{name} rows must hold num_kv_heads * head_dim elements")
+        if cache.device != key.device:
+            raise ValueError(f"{name} must be on the key's device")
+    if v_cache.shape != k_cache.shape:
+        raise ValueError("k_cache and v_cache shapes differ")
+    if value.dtype != key.dtype:
+        raise TypeError("key and value dtypes differ")
+    if not key.is_cuda or not slot_mapping.is_cuda or slot_mapping.device != key.device:
+        raise RuntimeError("store_kvcache expects CUDA tensors on one device")
+    if num_tokens == 0:
+        return
+    _native.call(
+        "mva_kv_store",
+        key.data_ptr(),
+        key.stride(0),
+        value.data_ptr(),
+        value.stride(0),
+        k_cache.data_ptr(),
+        v_cache.data_ptr(),
+        k_cache.numel() // row_elems,
+        slot_mapping.data_ptr(),
+        1 if slot_mapping.dtype == torch.int64 else 0,
+        num_tokens,
+        row_elems,
+        _native.dtype_code(key.dtype),
+        _native.stream_handle(key.device),
+    )
+
+
+def decode_workspace_bytes(num_seqs: int, num_part_slots: int, num_kv_heads: int, group: int) -> int:
+    return int(
+        _native.query("mva_decode_workspace_bytes", num_seqs, num_part_slots, num_kv_heads, group)
+    )
+
+
+def paged_decode(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    items: torch.Tensor,
+    num_items: int,
+    num_seqs: int,
+    num_part_slots: int,
+    out: torch.Tensor,
+    workspace: torch.Tensor | None,
+    softmax_scale: float,
+) -> None:
+    """Launch the paged GQA decode kernel over prepared work items.
+
+    ``q``/``out`` are ``[T, Hq, D]`` views (rows addressed by the items'
+    ``q_row``); caches ``[P, page, Hkv, D]``; ``items`` int32 ``[n, 8]``.
+    """
+    num_q_heads, head_dim = q.shape[1], q.shape[2]
+    num_pages, page_size, num_kv_heads = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
+    ws_ptr = workspace.data_ptr() if workspace is not None else 0
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _native.call(
+        "mva_paged_decode",
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k_cache.data_ptr(), v_cache.data_ptr(), num_pages, k_cache.stride(0), k_cache.stride(1),
+        block_tables.data_ptr(), block_tables.stride(0), seq_lens.data_ptr(),
+        items.data_ptr(), num_items, num_seqs, num_part_slots,
+        out.data_ptr(), out.stride(0), out.stride(1),
+        ws_ptr, ws_bytes,
+        num_q_heads, num_kv_heads, head_dim, page_size, float(softmax_scale),
+        _native.dtype_code(q.dtype), _native.stream_handle(q.device),
+    )
