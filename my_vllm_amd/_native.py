@@ -45,6 +45,30 @@ _SIGNATURES = {
             _i32, _i32, _i32, _i32, _f32, _i32, _c_void_p,  # heads, head_dim, page, scale, dtype, stream
         ],
     ),
+    "mva_prefill_tile_tokens": (_i32, [_i32, _i32]),
+    "mva_paged_prefill": (
+        _i32,
+        [
+            _c_void_p, _i64, _i64,  # q, q_token_stride, q_head_stride
+            _c_void_p, _c_void_p, _i64, _i64, _i64,  # k_cache, v_cache, num_pages, page_stride, token_stride
+            _c_void_p, _i64, _c_void_p, _c_void_p,  # block_tables, stride, seq_lens, query_start_loc
+            _c_void_p, _i64,  # items, num_items
+            _c_void_p, _i64, _i64,  # out, out_token_stride, out_head_stride
+            _i32, _i32, _i32, _i32, _f32, _i32, _c_void_p,
+        ],
+    ),
+    "mva_paged_mixed": (
+        _i32,
+        [
+            _c_void_p, _i64, _i64,
+            _c_void_p, _c_void_p, _i64, _i64, _i64,
+            _c_void_p, _i64, _c_void_p, _c_void_p,
+            _c_void_p, _i64, _c_void_p, _i64, _i64, _i64,  # prefill items, n, decode items, n, num_seqs, slots
+            _c_void_p, _i64, _i64,
+            _c_void_p, _i64,
+            _i32, _i32, _i32, _i32, _f32, _i32, _c_void_p,
+        ],
+    ),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

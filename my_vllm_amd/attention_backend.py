@@ -269,8 +269,9 @@ class MI355XAttentionMetadata:
 
     ``decode_items`` is int32 ``[num_decode_items, 8]`` (see
     ``make_decode_items``); ``None`` when the batch has no decode sequences.
-    ``kv_indptr`` is the page CSR offset list (host ints): sequence ``s`` owns
-    pages ``block_tables[s, :kv_indptr[s+1]-kv_indptr[s]]``.
+    ``prefill_items`` is int32 ``[num_prefill_items, 4]`` query tiles (see
+    ``make_prefill_items``).  ``kv_indptr`` is the page CSR offset list (host
+    ints): sequence ``s`` owns pages ``block_tables[s, :kv_indptr[s+1]-kv_indptr[s]]``.
     """
 
     query_start_loc: torch.Tensor
@@ -283,6 +284,8 @@ class MI355XAttentionMetadata:
     num_decode_items: int = 0
     num_decode_part_slots: int = 0
     decode_chunk_pages: int = 0
+    prefill_items: torch.Tensor | None = None
+    num_prefill_items: int = 0
 
     @property
     def is_cacheless(self) -> bool:
@@ -343,6 +346,34 @@ def make_decode_items(
     items[:, 6] = first_q_row + seq_local
     order = np.argsort(-(end - begin), kind="stable")
     return items[order], int(split_sizes.sum())
+
+
+def make_prefill_items(
+    query_upper: np.ndarray | list[int],
+    kv_upper: np.ndarray | list[int],
+    tile_tokens: int,
+) -> np.ndarray:
+    """Query tiles ``(seq, first_token, 0, 0)`` for prefill sequences ``0..S-1``.
+
+    ``query_upper[s]`` bounds the sequence's new-token count (exact when known;
+    tiles past the real count exit on the device) and ``kv_upper[s]`` its
+    context length.  Tiles are ordered by their estimated key count, largest
+    first, so long causal rows start early.
+    """
+    q_ub = np.asarray(query_upper, dtype=np.int64)
+    kv_ub = np.asarray(kv_upper, dtype=np.int64)
+    ntiles = np.maximum((q_ub + tile_tokens - 1) // tile_tokens, 1)
+    seq = np.repeat(np.arange(q_ub.size), ntiles)
+    first_tile = np.cumsum(ntiles) - ntiles
+    tile = np.arange(int(ntiles.sum())) - np.repeat(first_tile, ntiles)
+    start = tile * tile_tokens
+    end = np.minimum(start + tile_tokens, np.repeat(q_ub, ntiles))
+    cost = np.repeat(kv_ub - q_ub, ntiles) + end
+    items = np.zeros((seq.size, ops.PREFILL_ITEM_INTS), dtype=np.int32)
+    items[:, 0] = seq
+    items[:, 1] = start
+    order = np.argsort(-cost, kind="stable")
+    return items[order]
 
 
 def _to_device(array: np.ndarray, device: torch.device) -> torch.Tensor:
@@ -509,6 +540,26 @@ class MI355XAttentionBackendMixin:
             )
             num_decode_items = items.shape[0]
             decode_items = _to_device(items, block_tables.device)
+        prefill_items = None
+        num_prefill_items = 0
+        if common.num_prefill_seqs:
+            num_prefill = common.num_prefill_seqs
+            kv_ub = counts[:num_prefill] * self.block_size
+            if common.trusted:
+                # Only host ints are available: bound each sequence's query count.
+                q_ub = np.minimum(
+                    np.minimum(kv_ub, common.max_q_len),
+                    common.num_prefill_tokens - (num_prefill - 1),
+                )
+                q_ub = np.maximum(q_ub, 1)
+            else:
+                qsl = common.query_start_loc[: num_prefill + 1].cpu().numpy().astype(np.int64)
+                q_ub = qsl[1:] - qsl[:-1]
+                kv_ub = common.seq_lens[:num_prefill].cpu().numpy().astype(np.int64)
+            tile_tokens = ops.PREFILL_ROWS // (self.num_q_heads // self.num_kv_heads)
+            items = make_prefill_items(q_ub, kv_ub, tile_tokens)
+            num_prefill_items = items.shape[0]
+            prefill_items = _to_device(items, block_tables.device)
         return MI355XAttentionMetadata(
             query_start_loc=common.query_start_loc,
             seq_lens=common.seq_lens,
@@ -520,6 +571,8 @@ class MI355XAttentionBackendMixin:
             num_decode_items=num_decode_items,
             num_decode_part_slots=num_part_slots,
             decode_chunk_pages=chunk_pages,
+            prefill_items=prefill_items,
+            num_prefill_items=num_prefill_items,
         )
 
     def build_plan(self, common, metadata: MI355XAttentionMetadata | None = None):
@@ -665,11 +718,43 @@ class MI355XAttentionBackendMixin:
             self.softmax_scale,
         )
 
-    def _run_prefill(self, q, k_cache, v_cache, common, metadata, output) -> None:
-        raise NotImplementedError("MI355X prefill kernel is not built yet")
+    def _run_prefill(self, q, k_cache, v_cache, common, metadata: MI355XAttentionMetadata, output) -> None:
+        ops.paged_prefill(
+            q,
+            k_cache,
+            v_cache,
+            metadata.block_tables,
+            metadata.seq_lens,
+            metadata.query_start_loc,
+            metadata.prefill_items,
+            metadata.num_prefill_items,
+            output,
+            self.softmax_scale,
+        )
 
-    def _run_mixed(self, q, k_cache, v_cache, common, metadata, output) -> None:
-        raise NotImplementedError("MI355X mixed kernel is not built yet")
+    def _run_mixed(self, q, k_cache, v_cache, common, metadata: MI355XAttentionMetadata, output) -> None:
+        group = self.num_q_heads // self.num_kv_heads
+        ws_bytes = ops.decode_workspace_bytes(
+            common.num_seqs, metadata.num_decode_part_slots, self.num_kv_heads, group
+        )
+        workspace = self._get_workspace(ws_bytes, q.device)
+        ops.paged_mixed(
+            q,
+            k_cache,
+            v_cache,
+            metadata.block_tables,
+            metadata.seq_lens,
+            metadata.query_start_loc,
+            metadata.prefill_items,
+            metadata.num_prefill_items,
+            metadata.decode_items,
+            metadata.num_decode_items,
+            common.num_seqs,
+            metadata.num_decode_part_slots,
+            output,
+            workspace,
+            self.softmax_scale,
+        )
 
 
 class MI355XAttentionBackend(MI355XAttentionBackendMixin, AttentionBackend):
@@ -792,4 +877,5 @@ __all__ = [
     "MI355XSplitAttentionBackend",
     "choose_decode_chunk_pages",
     "make_decode_items",
+    "make_prefill_items",
 ]

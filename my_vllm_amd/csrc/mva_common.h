@@ -62,6 +62,36 @@ __device__ inline void st16(void* p, V v) {
   *reinterpret_cast<V*>(p) = v;
 }
 
+// LDS (address space 3) byte pointer.  Kernels pass LDS buffers around with
+// this type so every access compiles to ds_* instructions (a generic pointer
+// would compile to flat_* loads with 64-bit addresses).
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+template <typename V>
+__device__ inline V lds_ld16(const lds_u8* p) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) V*>(p);
+}
+template <typename V>
+__device__ inline void lds_st16(lds_u8* p, V v) {
+  *reinterpret_cast<__attribute__((address_space(3))) V*>(p) = v;
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane j receives element j%4
+// of the 8-byte rows supplied by lanes 4e + j/4 (e = 0..3); i.e. if lane i
+// points at row i/4, columns 4*(i%4)..+3 of a 4 x 16 block of 16-bit values,
+// lane j gets column j of the block.
+__device__ inline s16x4 lds_ld_tr16(const lds_u8* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
+}
+
+// 16-byte global -> LDS copy; lane i's bytes land at lds_base + 16*i.
+__device__ inline void dma16(const void* g, lds_u8* lds_base) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+}
+
 // Compiler-level ordering point for LDS traffic that is shared between lanes
 // of one wavefront.  LDS instructions of a wavefront execute in issue order,
 // so only the compiler has to be kept from reordering them.

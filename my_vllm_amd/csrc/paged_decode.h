@@ -101,7 +101,7 @@ __device__ inline int vlds_off(int t, int ch) { return t * 256 + ((ch ^ ((t & 7)
 // chunk lane%16.  16 vector-memory instructions per tile.
 template <typename T>
 __device__ inline void decode_load_tile(const DecodeParams& p, const T* kc, const T* vc, int page0,
-                                        int page1, int lane, DecodeTile<T>& tile, uint8_t* vlds) {
+                                        int page1, int lane, DecodeTile<T>& tile, lds_u8* vlds) {
   typedef typename Elem<T>::v8 V8;
   const int q4 = lane >> 4;
   const int c = lane & 15;
@@ -114,9 +114,7 @@ __device__ inline void decode_load_tile(const DecodeParams& p, const T* kc, cons
     for (int i = 0; i < 4; ++i) {
       const int t = 4 * i + q4;
       const int ch = c ^ ((t & 7) << 1);
-      __builtin_amdgcn_global_load_lds((const void*)(vp + t * p.tok_stride + 8 * ch),
-                                       (__attribute__((address_space(3))) void*)(vlds + pp * 4096 + 1024 * i),
-                                       16, 0, 0);
+      dma16(vp + t * p.tok_stride + 8 * ch, vlds + pp * 4096 + 1024 * i);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) tile.k[pp][j] = ld16<V8>(kp + c * p.tok_stride + 32 * q4 + 8 * j);
@@ -125,10 +123,8 @@ __device__ inline void decode_load_tile(const DecodeParams& p, const T* kc, cons
 
 template <typename T>
 __device__ void decode_item(const DecodeParams& p, const int32_t* __restrict__ it, int h,
-                            uint8_t* vbuf0, uint8_t* vbuf1) {
+                            lds_u8* vbuf0, lds_u8* vbuf1) {
   typedef typename Elem<T>::v8 V8;
-  typedef short s16x4 __attribute__((ext_vector_type(4)));
-  typedef short s16x8 __attribute__((ext_vector_type(8)));
   const int lane = threadIdx.x & 63;
   const int q4 = lane >> 4;
   const int c = lane & 15;
@@ -165,7 +161,7 @@ __device__ void decode_item(const DecodeParams& p, const int32_t* __restrict__ i
 
   // `edge` tiles contain masked tokens (sequence end, or an odd page past the
   // chunk end); the choice is wave-uniform and made per tile by `run`.
-  auto compute = [&](int t, const DecodeTile<T>& tile, const uint8_t* vbuf, auto edge_tag) {
+  auto compute = [&](int t, const DecodeTile<T>& tile, const lds_u8* vbuf, auto edge_tag) {
     constexpr bool edge = decltype(edge_tag)::value;
     const int pg0 = pb + 2 * t;
     f32x4 sc[2];
@@ -225,10 +221,8 @@ __device__ void decode_item(const DecodeParams& p, const int32_t* __restrict__ i
     for (int mt = 0; mt < 8; ++mt) {
       const int d = 16 * mt + dsub;
       const int off = vlds_off(tt, d >> 3) + (d & 7) * 2;
-      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(vbuf + off));
-      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(vbuf + 4096 + off));
+      const s16x4 lo = lds_ld_tr16(vbuf + off);
+      const s16x4 hi = lds_ld_tr16(vbuf + 4096 + off);
       s16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
       if constexpr (edge) {
         // Zero V of masked tokens so stale (possibly NaN) cache rows cannot
@@ -256,13 +250,13 @@ __device__ void decode_item(const DecodeParams& p, const int32_t* __restrict__ i
   // Tile t covers chunk pages 2t and 2t+1; a missing odd page and the
   // prefetch past the last tile re-read pages already in flight (cache hits)
   // and are masked or ignored, so every iteration issues the same loads.
-  auto load = [&](int t, DecodeTile<T>& tile, uint8_t* vbuf) {
+  auto load = [&](int t, DecodeTile<T>& tile, lds_u8* vbuf) {
     t = t < ntiles ? t : ntiles - 1;
     const int k0 = 2 * t;
     const int k1 = (2 * t + 1 < np) ? 2 * t + 1 : 2 * t;
     decode_load_tile<T>(p, kc, vc, page_at(k0), page_at(k1), lane, tile, vbuf);
   };
-  auto run = [&](int t, const DecodeTile<T>& tile, const uint8_t* vbuf) {
+  auto run = [&](int t, const DecodeTile<T>& tile, const lds_u8* vbuf) {
     const int pg0 = pb + 2 * t;
     if ((pg0 + 2 > pe) || ((pg0 + 2) * kPageSize > seq_len)) compute(t, tile, vbuf, std::true_type{});
     else compute(t, tile, vbuf, std::false_type{});

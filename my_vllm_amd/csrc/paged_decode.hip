@@ -14,12 +14,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
   // close together in time (the page's K/V are contiguous 32 KB runs).
   const int h = (int)(blockIdx.x % (uint32_t)p.num_kv_heads);
   const int item = (int)(blockIdx.x / (uint32_t)p.num_kv_heads);
-  decode_item<T>(p, p.items + (int64_t)item * kDecodeItemInts, h, vbuf0, vbuf1);
+  decode_item<T>(p, p.items + (int64_t)item * kDecodeItemInts, h, (lds_u8*)vbuf0, (lds_u8*)vbuf1);
 }
 
 }  // namespace
 
-int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+static int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
 // Workspace layout: [counters int32 num_seqs*Hkv][lse f32 slots*Hkv*G][o f32 slots*Hkv*G*D].
 int64_t decode_workspace_bytes(int64_t num_seqs, int64_t slots, int hkv, int group) {

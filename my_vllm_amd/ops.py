@@ -17,6 +17,10 @@ PAGE_SIZE = 16
 DECODE_ITEM_INTS = 8
 # Longest chunk one decode work item may cover (kMaxChunkPages).
 MAX_CHUNK_PAGES = 128
+# Query rows per prefill workgroup (kPrefillRows): G heads x 128 // G tokens.
+PREFILL_ROWS = 128
+# int32 fields per prefill work item (kPrefillItemInts).
+PREFILL_ITEM_INTS = 4
 
 
 def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
@@ -156,4 +160,78 @@ def paged_decode(
         ws_ptr, ws_bytes,
         num_q_heads, num_kv_heads, head_dim, page_size, float(softmax_scale),
         _native.dtype_code(q.dtype), _native.stream_handle(q.device),
+    )
+
+
+def _paged_args(q, k_cache, v_cache, block_tables, seq_lens):
+    return (
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0], k_cache.stride(0), k_cache.stride(1),
+        block_tables.data_ptr(), block_tables.stride(0), seq_lens.data_ptr(),
+    )
+
+
+def _tail_args(q, k_cache, softmax_scale):
+    return (
+        q.shape[1], k_cache.shape[2], q.shape[2], k_cache.shape[1], float(softmax_scale),
+        _native.dtype_code(q.dtype), _native.stream_handle(q.device),
+    )
+
+
+def paged_prefill(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    query_start_loc: torch.Tensor,
+    items: torch.Tensor,
+    num_items: int,
+    out: torch.Tensor,
+    softmax_scale: float,
+) -> None:
+    """Launch the ragged causal prefill kernel over prepared query tiles.
+
+    ``items`` int32 ``[n, 4]`` = (sequence, first query token of the tile, 0, 0);
+    tiles past a sequence's query count exit without writing.
+    """
+    _native.call(
+        "mva_paged_prefill",
+        *_paged_args(q, k_cache, v_cache, block_tables, seq_lens),
+        query_start_loc.data_ptr(),
+        items.data_ptr(), num_items,
+        out.data_ptr(), out.stride(0), out.stride(1),
+        *_tail_args(q, k_cache, softmax_scale),
+    )
+
+
+def paged_mixed(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    query_start_loc: torch.Tensor,
+    prefill_items: torch.Tensor,
+    num_prefill_items: int,
+    decode_items: torch.Tensor,
+    num_decode_items: int,
+    num_seqs: int,
+    num_part_slots: int,
+    out: torch.Tensor,
+    workspace: torch.Tensor | None,
+    softmax_scale: float,
+) -> None:
+    """One launch: prefill tiles write ``out[:P]``, decode items write ``out[P:]``."""
+    ws_ptr = workspace.data_ptr() if workspace is not None else 0
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _native.call(
+        "mva_paged_mixed",
+        *_paged_args(q, k_cache, v_cache, block_tables, seq_lens),
+        query_start_loc.data_ptr(),
+        prefill_items.data_ptr(), num_prefill_items,
+        decode_items.data_ptr(), num_decode_items, num_seqs, num_part_slots,
+        out.data_ptr(), out.stride(0), out.stride(1),
+        ws_ptr, ws_bytes,
+        *_tail_args(q, k_cache, softmax_scale),
     )

@@ -1,0 +1,148 @@
+"""Ragged causal chunked prefill (PREFILL route) on gfx950 vs the fp32 oracle.
+
+Tolerance 2e-2 absolute / 1e-2 relative (tests/_util.py).  Cases: the
+reference's shapes, the Qwen3-8B prefill-with-prefix configuration (a subset
+of its sequences is checked on the CPU), GQA ratios 1..16 including 3, a
+single-token chunk with a long context, unaligned prefixes, NaN-poisoned
+stale rows, fp16, trusted vs untrusted metadata, and the cacheless warmup.
+"""
+
+import pytest
+import torch
+
+from my_vllm_amd.attention_backend import AttentionRoute, MI355XAttentionBackend
+from my_vllm_amd.context import BatchType
+from my_vllm_amd.workloads import config_prefill, make_paged_batch
+from oracle.reference import paged_attention, ragged_attention
+from tests._util import assert_attention_close
+
+pytestmark = pytest.mark.gpu
+
+
+def to_device(batch, device, trusted=True):
+    c = batch.common
+    common = type(c)(**{**c.__dict__,
+                        "query_start_loc": c.query_start_loc.to(device),
+                        "seq_lens": c.seq_lens.to(device),
+                        "slot_mapping": c.slot_mapping.to(device),
+                        "block_tables": c.block_tables.to(device),
+                        "trusted": trusted})
+    return common, batch.q.to(device), batch.k_cache.to(device), batch.v_cache.to(device)
+
+
+def run_backend(batch, device, dtype=torch.bfloat16, trusted=True, mode="unified"):
+    hq, hkv = batch.q.shape[1], batch.k_cache.shape[2]
+    backend = MI355XAttentionBackend(hq, hkv, 128, 16, dtype, attention_mode=mode)
+    common, q, kc, vc = to_device(batch, device, trusted)
+    plan = backend.build_plan(common)
+    empty = q.new_empty((0, hkv, 128))
+    out = backend.forward(q, empty, empty, kc, vc, plan)
+    assert out.shape == q.shape and out.dtype == dtype
+    return out, plan
+
+
+def expected(batch, seqs=None):
+    if seqs is None:
+        return paged_attention(batch.q, batch.k_cache, batch.v_cache, batch.common.block_tables,
+                               batch.query_lengths, batch.kv_lengths)
+    rows, parts = [], []
+    starts = [0]
+    for n in batch.query_lengths:
+        starts.append(starts[-1] + n)
+    for s in seqs:
+        bt = batch.common.block_tables[s:s + 1]
+        q = batch.q[starts[s]:starts[s + 1]]
+        parts.append(paged_attention(q, batch.k_cache, batch.v_cache, bt,
+                                     [batch.query_lengths[s]], [batch.kv_lengths[s]]))
+        rows.extend(range(starts[s], starts[s + 1]))
+    return torch.cat(parts), rows
+
+
+def test_reference_shapes(gpu):
+    batch = make_paged_batch(307, [5, 3], [21, 13], 2, 16, 4)
+    out, plan = run_backend(batch, gpu)
+    assert plan.batch_type is BatchType.PURE_PREFILL and plan.route is AttentionRoute.PREFILL
+    assert_attention_close(out, expected(batch))
+
+
+def test_qwen3_8b_prefill_with_prefix_configuration(gpu):
+    batch = config_prefill(seed=2)
+    out, _ = run_backend(batch, gpu)
+    longest = max(range(16), key=lambda s: batch.kv_lengths[s])
+    seqs = sorted({0, 7, 15, longest})
+    exp, rows = expected(batch, seqs)
+    assert_attention_close(out.cpu()[rows], exp)
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (32, 8), (64, 8), (128, 8), (12, 4), (16, 1)])
+def test_gqa_ratios(gpu, hq, hkv):
+    q = [1, 37, 130, 64]
+    kv = [1, 37 + 16 * 3, 130 + 5, 64 + 200]
+    batch = make_paged_batch(61, q, kv, 4, hq, hkv)
+    out, _ = run_backend(batch, gpu)
+    assert_attention_close(out, expected(batch))
+
+
+def test_edge_lengths(gpu):
+    # single-token chunk over a long context, unaligned prefixes, exact tile
+    # and page multiples, q == kv (no prefix)
+    q = [1, 7, 32, 33, 96, 257, 64, 500]
+    kv = [2049, 7, 32 + 16, 33 + 1, 96 + 63, 257 + 1000, 64 + 64, 500 + 17]
+    batch = make_paged_batch(67, q, kv, len(q), 32, 8)
+    out, _ = run_backend(batch, gpu)
+    assert_attention_close(out, expected(batch))
+
+
+def test_untrusted_metadata_matches_trusted(gpu):
+    batch = make_paged_batch(71, [40, 300, 3], [100, 300, 70], 3, 32, 8)
+    a, _ = run_backend(batch, gpu, trusted=True)
+    a = a.clone()
+    b, _ = run_backend(batch, gpu, trusted=False)
+    assert torch.equal(a, b)
+    assert_attention_close(b, expected(batch))
+
+
+def test_stale_nan_rows_past_seq_len_do_not_leak(gpu):
+    q = [20, 70, 5]
+    kv = [40, 75, 150]
+    batch = make_paged_batch(73, q, kv, 3, 16, 8, extra_pages=2)
+    bt = batch.common.block_tables
+    for s, n in enumerate(kv):
+        last = int(bt[s, (n - 1) // 16])
+        batch.k_cache[last, (n - 1) % 16 + 1:] = float("nan")
+        batch.v_cache[last, (n - 1) % 16 + 1:] = float("nan")
+    used = set(bt[bt >= 0].tolist())
+    for p in range(batch.k_cache.shape[0]):
+        if p not in used:
+            batch.k_cache[p] = float("nan")
+            batch.v_cache[p] = float("nan")
+    out, _ = run_backend(batch, gpu)
+    assert_attention_close(out, expected(batch))
+
+
+def test_fp16(gpu):
+    batch = make_paged_batch(79, [100, 17], [180, 17], 2, 32, 8, dtype=torch.float16)
+    out, _ = run_backend(batch, gpu, dtype=torch.float16)
+    assert_attention_close(out, expected(batch))
+
+
+def test_cacheless_warmup_route(gpu):
+    torch.manual_seed(223)
+    lengths = [3, 1]
+    q = torch.randn(4, 16, 128).bfloat16()
+    k = torch.randn(4, 4, 128).bfloat16()
+    v = torch.randn(4, 4, 128).bfloat16()
+    from my_vllm_amd.context import CommonAttentionMetadata
+
+    common = CommonAttentionMetadata(
+        num_prefill_seqs=2, num_decode_seqs=0, num_prefill_tokens=4, num_decode_tokens=0,
+        query_start_loc=torch.tensor([0, 3, 4], dtype=torch.int32, device=gpu),
+        seq_lens=torch.tensor(lengths, dtype=torch.int32, device=gpu),
+        slot_mapping=torch.full((4,), -1, dtype=torch.int32, device=gpu),
+        block_tables=None, max_q_len=3, max_kv_len=3, trusted=True)
+    backend = MI355XAttentionBackend(16, 4, 128, 16, torch.bfloat16)
+    plan = backend.build_plan(common)
+    assert plan.route is AttentionRoute.WARMUP
+    empty = torch.empty(0, device=gpu)
+    out = backend.forward(q.to(gpu), k.to(gpu), v.to(gpu), empty, empty, plan)
+    assert_attention_close(out, ragged_attention(q, k, v, lengths))
