@@ -1,0 +1,297 @@
+"""Benchmark of the MI355X ragged-batch attention hot path (one GPU).
+
+Headline (``value``): one step = slot_mapping KV store + PURE_DECODE paged GQA
+attention at the Qwen3-0.6B shape (16 Q / 8 KV heads, head_dim 128, bf16,
+16-token pages, 64 sequences with contexts uniform in [128, 2048], seed 1),
+reported as algorithmic HBM GB/s of the whole step.  Inputs are resident in
+HBM before timing; four copies of the KV cache are rotated so the 256 MB
+Infinity Cache cannot serve a step from the previous one.
+
+Also reported (``extra``): SiLU-and-mul GB/s (4096 x 6144 and 8192 x 51200),
+PURE_PREFILL TFLOP/s (Qwen3-8B, 16 sequences with prefixes), MIXED tokens/s
+(single launch vs split launches) and long-context decode GB/s (Qwen3-32B,
+batch 128, contexts 8K-32K).  ``roofline`` covers the decode kernel alone,
+timed with HIP events on the stream it is launched on; ``cpu_baseline`` times
+the CPU oracle (the reference's fp32 paged-attention restatement) on a
+bounded sample of the same workload on the host cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBPS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "paged GQA decode HBM GB/s (% of peak); mixed-batch attention tokens/s"
+
+
+def parse_args(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-extra", action="store_true", help="headline and roofline only")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
+    return ap.parse_args(argv)
+
+
+def to_device(batch, device):
+    c = batch.common
+    common = type(c)(**{**c.__dict__,
+                        "query_start_loc": c.query_start_loc.to(device),
+                        "seq_lens": c.seq_lens.to(device),
+                        "slot_mapping": c.slot_mapping.to(device),
+                        "block_tables": c.block_tables.to(device)})
+    return common
+
+
+def time_launches(fn, iters: int, warmup: int) -> float:
+    """Average ms per call of `fn`, timed with HIP events on the current stream."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(iters):
+        fn(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def decode_bytes(batch, num_q_heads, num_kv_heads, elem=2) -> int:
+    """Algorithmic bytes of one decode launch: unique K/V rows read, q read,
+    o written, page ids and seq_lens read."""
+    kv = sum(batch.kv_lengths) * num_kv_heads * 128 * elem * 2
+    qo = 2 * len(batch.kv_lengths) * num_q_heads * 128 * elem
+    meta = sum(batch.block_counts) * 4 + len(batch.kv_lengths) * 4
+    return kv + qo + meta
+
+
+def store_bytes(num_tokens, num_kv_heads, elem=2) -> int:
+    """KV store: read K and V rows, write them to the cache, read slots."""
+    return num_tokens * (4 * num_kv_heads * 128 * elem + 4)
+
+
+def causal_pairs(q_lens, kv_lens) -> int:
+    return sum(q * (kv - q) + q * (q + 1) // 2 for q, kv in zip(q_lens, kv_lens))
+
+
+def headline(args, device):
+    from my_vllm_amd import ops
+    from my_vllm_amd.attention import KVCacheStore
+    from my_vllm_amd.attention_backend import MI355XAttentionBackend
+    from my_vllm_amd.custom_op import CustomOpConfig
+    from my_vllm_amd.workloads import config_decode_small
+
+    batch = config_decode_small(seed=1)
+    hq, hkv = 16, 8
+    common = to_device(batch, device)
+    q = batch.q.to(device)
+    k_new, v_new = batch.k_new.to(device), batch.v_new.to(device)
+    copies = 4
+    caches = [(batch.k_cache.to(device), batch.v_cache.to(device)) for _ in range(copies)]
+    backend = MI355XAttentionBackend(hq, hkv, 128, 16, torch.bfloat16)
+    store = KVCacheStore(CustomOpConfig(platform="cuda"))
+    plan = backend.build_plan(common)
+    empty = q.new_empty((0, hkv, 128))
+
+    def step(i):
+        kc, vc = caches[i % copies]
+        store(k_new, v_new, kc, vc, common.slot_mapping)
+        backend.forward(q, empty, empty, kc, vc, plan)
+
+    torch.cuda.synchronize()
+    ms_step = time_launches(step, args.steps, args.warmup)
+    step_bytes = decode_bytes(batch, hq, hkv) + store_bytes(len(batch.kv_lengths), hkv)
+
+    # Roofline of the decode kernel alone: direct launches (no store), same
+    # rotation, timed on the launch stream.
+    md = plan.metadata
+    out = torch.empty_like(q)
+    ws = backend._get_workspace(
+        ops.decode_workspace_bytes(common.num_seqs, md.num_decode_part_slots, hkv, hq // hkv), device)
+
+    def decode_only(i):
+        kc, vc = caches[i % copies]
+        ops.paged_decode(q, kc, vc, md.block_tables, md.seq_lens, md.decode_items, md.num_decode_items,
+                         md.num_decode_waves, common.num_seqs,
+                         md.num_decode_part_slots, out, ws, backend.softmax_scale)
+
+    ms_decode = time_launches(decode_only, max(args.steps, 200), args.warmup)
+    dec_bytes = decode_bytes(batch, hq, hkv)
+    achieved = dec_bytes / ms_decode / 1e6
+    return {
+        "ms_per_step": ms_step,
+        "value": step_bytes / ms_step / 1e6,
+        "decode_ms": ms_decode,
+        "decode_bytes": dec_bytes,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "kernel": "paged_decode_kernel<bf16>",
+            "bytes_per_launch": dec_bytes,
+            "avg_launch_ms": round(ms_decode, 5),
+        },
+        "batch": batch,
+        "waves": md.num_decode_waves,
+        "items": md.num_decode_items,
+    }
+
+
+def cpu_baseline(batch, seconds: float):
+    """The CPU oracle (fp32 paged attention, the reference's test restatement)
+    on the first 16 sequences of the headline batch, as K/V GB/s."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle.reference import paged_attention
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    n = 16
+    q_rows = sum(batch.query_lengths[:n])
+    args = (batch.q[:q_rows], batch.k_cache, batch.v_cache, batch.common.block_tables[:n],
+            batch.query_lengths[:n], batch.kv_lengths[:n])
+    paged_attention(*args)  # warm up
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        paged_attention(*args)
+        reps += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    kv_bytes = sum(batch.kv_lengths[:n]) * 8 * 128 * 2 * 2
+    return {
+        "value": round(kv_bytes / dt / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"oracle.reference.paged_attention (fp32 einsum) on sequences 0-15 of the headline "
+                  f"batch ({sum(batch.kv_lengths[:n])} keys), {reps} reps in {seconds:.0f}s",
+    }
+
+
+def extra_measurements(device, steps: int):
+    from my_vllm_amd import ops
+    from my_vllm_amd.attention_backend import MI355XAttentionBackend
+    from my_vllm_amd.workloads import config_long_decode, config_mixed, config_prefill, silu_input
+
+    res = {}
+    # SiLU-and-mul, Qwen3-0.6B MLP: 8 rotating inputs (600 MB > Infinity Cache).
+    x = silu_input(4096, 6144, seed=0).to(device)
+    xs = [x.clone() for _ in range(8)]
+    ms = time_launches(lambda i: ops.silu_and_mul(xs[i % 8]), 400, 20)
+    res["silu_4096x6144_GBps"] = round(75497472 / ms / 1e6, 1)
+    del xs, x
+    # SiLU-and-mul at intermediate 25600, 8192 tokens.
+    x5 = silu_input(8192, 51200, seed=4, device=device, rng_device="cuda")
+    ms = time_launches(lambda i: ops.silu_and_mul(x5), 50, 5)
+    res["silu_8192x51200_GBps"] = round(8192 * 51200 * 2 * 1.5 / ms / 1e6, 1)
+    del x5
+
+    def attn_case(batch, hq, hkv, mode="unified", iters=20):
+        backend = MI355XAttentionBackend(hq, hkv, 128, 16, torch.bfloat16, attention_mode=mode)
+        common = to_device(batch, device)
+        q = batch.q.to(device)
+        kc, vc = batch.k_cache.to(device), batch.v_cache.to(device)
+        plan = backend.build_plan(common)
+        empty = q.new_empty((0, hkv, 128))
+        return time_launches(lambda i: backend.forward(q, empty, empty, kc, vc, plan), iters, 3)
+
+    # PURE_PREFILL with prefix, Qwen3-8B.
+    batch = config_prefill(seed=2, device=device, rng_device="cuda")
+    ms = attn_case(batch, 32, 8)
+    flops = 4 * 128 * 32 * causal_pairs(batch.query_lengths, batch.kv_lengths)
+    res["prefill_TFLOPs"] = round(flops / ms / 1e9, 1)
+    res["prefill_ms"] = round(ms, 4)
+    del batch
+
+    # MIXED, Qwen3-8B, token budget 8192.
+    batch = config_mixed(seed=3, device=device, rng_device="cuda")
+    t = sum(batch.query_lengths)
+    ms_u = attn_case(batch, 32, 8, "unified")
+    ms_s = attn_case(batch, 32, 8, "split")
+    dec_bytes = sum(batch.kv_lengths[4:]) * 8 * 128 * 2 * 2
+    pf_flops = 4 * 128 * 32 * causal_pairs(batch.query_lengths[:4], batch.kv_lengths[:4])
+    bound_ms = max(dec_bytes / HBM_PEAK_GBPS / 1e6, pf_flops / BF16_PEAK_TFLOPS / 1e9)
+    res["mixed_tokens"] = t
+    res["mixed_unified_tokens_per_s"] = round(t / ms_u * 1e3, 1)
+    res["mixed_split_tokens_per_s"] = round(t / ms_s * 1e3, 1)
+    res["mixed_unified_ms"] = round(ms_u, 4)
+    res["mixed_split_ms"] = round(ms_s, 4)
+    res["mixed_unified_roofline_frac"] = round(bound_ms / ms_u, 4)
+    del batch
+
+    # Long-context decode, Qwen3-32B (one layer's KV, ~10.7 GB).
+    batch = config_long_decode(seed=4, device=device, rng_device="cuda")
+    ms = attn_case(batch, 64, 8, iters=10)
+    gbps = decode_bytes(batch, 64, 8) / ms / 1e6
+    res["long_decode_GBps"] = round(gbps, 1)
+    res["long_decode_frac"] = round(gbps / HBM_PEAK_GBPS, 4)
+    del batch
+    torch.cuda.empty_cache()
+    return res
+
+
+def main(argv=None):
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one MI355X only; --gpus {args.gpus} is not supported "
+            "(attention shards by KV head with no exchange; see the design notes)",
+            file=sys.stderr,
+        )
+        return 2
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    from my_vllm_amd import _native
+
+    _native.load_library()  # fails loudly when the gfx950 library is missing
+    head = headline(args, device)
+    extra = {} if args.no_extra else extra_measurements(device, args.steps)
+    cpu = cpu_baseline(head["batch"], args.cpu_seconds)
+    value = head["value"]
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: N(0,1) values, seeded lengths and page permutations",
+        "config": {
+            "workload": "slot_mapping KV store + PURE_DECODE paged GQA attention, 16 Q / 8 KV heads, "
+                        "head_dim 128, bf16, page 16, 64 seqs, ctx U[128,2048] (seed 1), "
+                        "4 rotated KV-cache copies",
+            "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBPS, 2),
+            "decode_waves": head["waves"],
+            "decode_pieces": head["items"],
+        },
+        "roofline": head["roofline"],
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

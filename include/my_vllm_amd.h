@@ -61,8 +61,10 @@ int mva_kv_store(const void* key, int64_t key_row_stride, const void* value,
 
 /*
  * Bytes of device workspace mva_paged_decode needs for `num_seqs` sequences
- * and `num_part_slots` split-K partial slots.  The workspace must be zeroed
- * once when first allocated; the kernels leave it zeroed again on return.
+ * and `num_part_slots` split-K partial slots (a 256-byte scheduler area,
+ * per-(sequence, KV head) arrival counters, partial outputs).  The workspace
+ * must be zeroed once when first allocated; the kernels leave its counters
+ * zeroed again on return.  Launches that share a workspace must not overlap.
  */
 int64_t mva_decode_workspace_bytes(int64_t num_seqs, int64_t num_part_slots, int num_kv_heads,
                                    int group);
@@ -74,15 +76,19 @@ int64_t mva_decode_workspace_bytes(int64_t num_seqs, int64_t num_part_slots, int
  *   q:    query rows; q + row*q_token_stride + head*q_head_stride.
  *   block_tables [num_seqs, block_table_stride] int32 page ids; seq_lens
  *         [num_seqs] int32 context lengths (including the new token).
- *   items [num_items, 8] int32 work items, each
- *         {seq, page_begin, page_end, chunk, n_chunks, part_base, q_row, 0}:
- *         pages [page_begin, page_end) of sequence `seq` (at most 128 pages),
- *         chunk `chunk` of `n_chunks`; partial slots part_base .. part_base +
- *         n_chunks - 1 (unused when n_chunks == 1); output row q_row.
+ *   items [num_items, 8] int32 pieces, each
+ *         {seq, page_begin, page_end, chunk, n_chunks, part_base, q_row, kv_head}:
+ *         pages [page_begin, page_end) of (sequence `seq`, KV head `kv_head`)
+ *         (at most 128 pages), piece `chunk` of `n_chunks`; split-K partial
+ *         slots part_base .. part_base + n_chunks - 1 (unused when
+ *         n_chunks == 1); output row q_row.
+ *   num_waves (1 .. num_items): wavefronts launched; wavefront w starts on
+ *         piece w and then claims pieces num_waves, num_waves + 1, ... from a
+ *         counter in the workspace, so pieces should be listed longest first.
  *   out:  out + row*out_token_stride + head*out_head_stride, `dtype`.
  * softmax over keys j < seq_len with scale `softmax_scale`; fp32 accumulate.
- * Launch grid = num_items x num_kv_heads wavefronts; split chunks are merged
- * in the same launch.  Requires head_dim 128, page_size 16, num_q_heads /
+ * The pieces of one (sequence, KV head) are merged in the same launch by the
+ * last one to finish.  Requires head_dim 128, page_size 16, num_q_heads /
  * num_kv_heads <= 16, 16-byte aligned q/cache buffers and strides.
  * Replaces FlashInfer BatchDecodeWithPagedKVCacheWrapper.plan/run as used by
  * the reference's DECODE route (nanovllm/layers/attention_backend.py:826-840,
@@ -92,10 +98,57 @@ int mva_paged_decode(const void* q, int64_t q_token_stride, int64_t q_head_strid
                      const void* k_cache, const void* v_cache, int64_t num_pages,
                      int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
                      int64_t block_table_stride, const int32_t* seq_lens, const int32_t* items,
-                     int64_t num_items, int64_t num_seqs, int64_t num_part_slots, void* out,
+                     int64_t num_items, int64_t num_waves, int64_t num_seqs,
+                     int64_t num_part_slots, void* out,
                      int64_t out_token_stride, int64_t out_head_stride, void* workspace,
                      int64_t workspace_bytes, int num_q_heads, int num_kv_heads, int head_dim,
                      int page_size, float softmax_scale, int dtype, void* stream);
+
+/* Query-token rows per prefill workgroup tile for a GQA ratio (128 / ratio),
+ * or -1 for invalid head counts. */
+int mva_prefill_tile_tokens(int num_q_heads, int num_kv_heads);
+
+/*
+ * Ragged causal chunked prefill over prefix-cached pages (same cache and q/out
+ * conventions as mva_paged_decode).  Sequence s has query rows
+ * query_start_loc[s] .. query_start_loc[s+1] - 1 (q_s rows) and seq_lens[s]
+ * keys including them; query i sees keys j <= seq_lens[s] - q_s + i.  The new
+ * tokens' K/V are read from the cache (store them first).
+ *   items [num_items, 4] int32 query tiles {seq, first_token, 0, 0}; a tile
+ *         covers mva_prefill_tile_tokens() tokens x all query heads of one KV
+ *         head; tiles past a sequence's query count exit without writing.
+ * Launch grid = num_items x num_kv_heads workgroups of 256 threads.
+ * Replaces FlashInfer BatchPrefillWithPagedKVCacheWrapper.plan/run on the
+ * reference's PREFILL route (nanovllm/layers/attention_backend.py:810-825,
+ * :992-994) and the prefill half of MIXED_SPLIT (:858-873, :1015-1019).
+ */
+int mva_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                      const void* k_cache, const void* v_cache, int64_t num_pages,
+                      int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
+                      int64_t block_table_stride, const int32_t* seq_lens,
+                      const int32_t* query_start_loc, const int32_t* items, int64_t num_items,
+                      void* out, int64_t out_token_stride, int64_t out_head_stride,
+                      int num_q_heads, int num_kv_heads, int head_dim, int page_size,
+                      float softmax_scale, int dtype, void* stream);
+
+/*
+ * MIXED batch in one launch: prefill tiles (as mva_paged_prefill) write the
+ * rows of the leading prefill sequences and decode pieces (as
+ * mva_paged_decode) write the trailing decode rows of the same `out` buffer.
+ * Replaces FlashInfer BatchAttention.plan/run on the reference's MIXED_UNIFIED
+ * route (nanovllm/layers/attention_backend.py:841-857, :998-1009).
+ */
+int mva_paged_mixed(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                    const void* k_cache, const void* v_cache, int64_t num_pages,
+                    int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
+                    int64_t block_table_stride, const int32_t* seq_lens,
+                    const int32_t* query_start_loc, const int32_t* prefill_items,
+                    int64_t num_prefill_items, const int32_t* decode_items,
+                    int64_t num_decode_items, int64_t num_decode_waves, int64_t num_seqs,
+                    int64_t num_part_slots,
+                    void* out, int64_t out_token_stride, int64_t out_head_stride,
+                    void* workspace, int64_t workspace_bytes, int num_q_heads, int num_kv_heads,
+                    int head_dim, int page_size, float softmax_scale, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -267,8 +267,9 @@ MAX_GROUP = 16
 class MI355XAttentionMetadata:
     """Backend-private per-step metadata: device work lists built on the host.
 
-    ``decode_items`` is int32 ``[num_decode_items, 8]`` (see
-    ``make_decode_items``); ``None`` when the batch has no decode sequences.
+    ``decode_items`` is int32 ``[num_decode_items, 8]`` pieces, claimed by
+    ``num_decode_waves`` wavefronts (see ``make_decode_plan``); ``None``
+    without decode sequences.
     ``prefill_items`` is int32 ``[num_prefill_items, 4]`` query tiles (see
     ``make_prefill_items``).  ``kv_indptr`` is the page CSR offset list (host
     ints): sequence ``s`` owns pages ``block_tables[s, :kv_indptr[s+1]-kv_indptr[s]]``.
@@ -282,8 +283,8 @@ class MI355XAttentionMetadata:
     num_prefill_pages: int
     decode_items: torch.Tensor | None = None
     num_decode_items: int = 0
+    num_decode_waves: int = 0
     num_decode_part_slots: int = 0
-    decode_chunk_pages: int = 0
     prefill_items: torch.Tensor | None = None
     num_prefill_items: int = 0
 
@@ -292,60 +293,81 @@ class MI355XAttentionMetadata:
         return self.block_tables is None
 
 
-def choose_decode_chunk_pages(total_pages: int, num_kv_heads: int) -> int:
-    """Pages per decode work item.
+_RESIDENT_DECODE_WAVES_PER_CU = 8  # 2 per SIMD at the decode kernel's register budget
 
-    Short batches are cut fine so that enough wavefronts stream at once
-    (256 CUs x 8 resident decode waves); long contexts use long chunks to keep
-    the split-K partial traffic small.  Always even and within [8, 128].
-    ``MVA_DECODE_CHUNK_PAGES`` overrides the choice.
-    """
-    override = os.environ.get("MVA_DECODE_CHUNK_PAGES")
+
+def resident_decode_waves(device: torch.device | None = None) -> int:
+    """Decode wavefronts the GPU holds at once (CUs x 8); 2048 on MI355X."""
+    override = os.environ.get("MVA_DECODE_WAVES")
     if override:
-        pages = int(override)
-    else:
-        target_items = 8192
-        pages = -(-total_pages * num_kv_heads // target_items)
-    pages = max(8, min(ops.MAX_CHUNK_PAGES, pages))
-    return pages + (pages & 1)
+        return max(1, int(override))
+    if device is not None and device.type == "cuda":
+        return torch.cuda.get_device_properties(device).multi_processor_count * _RESIDENT_DECODE_WAVES_PER_CU
+    return 256 * _RESIDENT_DECODE_WAVES_PER_CU
 
 
-def make_decode_items(
+def make_decode_plan(
     block_counts: np.ndarray | tuple[int, ...],
     first_seq: int,
     first_q_row: int,
-    chunk_pages: int,
-) -> tuple[np.ndarray, int]:
-    """Decode work items for sequences ``first_seq + i`` with ``block_counts[i]`` pages.
+    num_kv_heads: int,
+    num_waves: int,
+    pieces_per_wave: int = 4,
+    min_piece_pages: int = 4,
+    max_piece_pages: int = ops.MAX_CHUNK_PAGES,
+) -> tuple[np.ndarray, int, int]:
+    """Cut a decode batch into pieces that wavefronts claim dynamically.
 
-    Each item is ``(seq, page_begin, page_end, chunk, n_chunks, part_base,
-    q_row, 0)``; sequence ``first_seq + i`` reads query row ``first_q_row + i``.
-    Items are ordered longest first.  Returns ``(items, num_part_slots)``.
+    Sequence ``first_seq + i`` has ``block_counts[i]`` pages and reads query
+    row ``first_q_row + i``.  Every (sequence, KV head) segment of ``L`` pages
+    is cut into ``ceil(L / P)`` near-equal pieces, with the piece length ``P``
+    chosen so that ``num_waves`` wavefronts see about ``pieces_per_wave``
+    pieces each (clamped to ``[min_piece_pages, max_piece_pages]``); short
+    pieces let the wavefronts on faster CUs take more of the work.  A piece
+    is ``(seq, page_begin, page_end, chunk, n_chunks, part_base, q_row,
+    kv_head)``; a segment cut into ``n_chunks > 1`` pieces owns that many
+    split-K partial slots from ``part_base``.  Pieces are ordered longest
+    first, then sequence-major with the KV head fastest (the head slices of
+    one page are neighbours in the cache).  Returns ``(items, waves,
+    num_part_slots)`` with ``waves = min(num_waves, len(items))``, the grid to
+    launch.
     """
     counts = np.asarray(block_counts, dtype=np.int64)
     if counts.size == 0:
-        return np.zeros((0, ops.DECODE_ITEM_INTS), dtype=np.int32), 0
-    nchunks = (counts + chunk_pages - 1) // chunk_pages
-    nchunks = np.maximum(nchunks, 1)
-    total = int(nchunks.sum())
-    seq_local = np.repeat(np.arange(counts.size), nchunks)
-    first_item = np.cumsum(nchunks) - nchunks
-    chunk = np.arange(total) - np.repeat(first_item, nchunks)
-    begin = chunk * chunk_pages
-    end = np.minimum(begin + chunk_pages, np.repeat(counts, nchunks))
-    split = nchunks > 1
-    split_sizes = np.where(split, nchunks, 0)
-    part_base_seq = np.cumsum(split_sizes) - split_sizes
-    items = np.zeros((total, ops.DECODE_ITEM_INTS), dtype=np.int32)
-    items[:, 0] = first_seq + seq_local
+        return np.zeros((0, ops.DECODE_ITEM_INTS), np.int32), 0, 0
+    if np.any(counts <= 0):
+        raise ValueError("every decode sequence needs at least one page")
+    if not 1 <= min_piece_pages <= max_piece_pages <= ops.MAX_CHUNK_PAGES:
+        raise ValueError("piece length bounds must satisfy 1 <= min <= max <= 128")
+    seg_len = np.repeat(counts, num_kv_heads)
+    nseg = seg_len.size
+    total = int(seg_len.sum())
+    target = max(1, int(num_waves) * max(1, int(pieces_per_wave)))
+    piece = int(np.clip(-(-total // target), min_piece_pages, max_piece_pages))
+    nchunks = (seg_len + piece - 1) // piece
+    seg_of = np.repeat(np.arange(nseg), nchunks)
+    first_piece = np.cumsum(nchunks) - nchunks
+    chunk = np.arange(int(nchunks.sum())) - np.repeat(first_piece, nchunks)
+    n_of = nchunks[seg_of]
+    len_of = seg_len[seg_of]
+    # Near-equal cut of L pages into n pieces: piece k covers [k*L//n, (k+1)*L//n).
+    begin = (chunk * len_of) // n_of
+    end = ((chunk + 1) * len_of) // n_of
+    split_sizes = np.where(nchunks > 1, nchunks, 0)
+    part_base = np.cumsum(split_sizes) - split_sizes
+    items = np.zeros((seg_of.size, ops.DECODE_ITEM_INTS), dtype=np.int32)
+    items[:, 0] = first_seq + seg_of // num_kv_heads
     items[:, 1] = begin
     items[:, 2] = end
     items[:, 3] = chunk
-    items[:, 4] = np.repeat(nchunks, nchunks)
-    items[:, 5] = np.repeat(part_base_seq, nchunks)
-    items[:, 6] = first_q_row + seq_local
+    items[:, 4] = n_of
+    items[:, 5] = part_base[seg_of]
+    items[:, 6] = first_q_row + seg_of // num_kv_heads
+    items[:, 7] = seg_of % num_kv_heads
     order = np.argsort(-(end - begin), kind="stable")
-    return items[order], int(split_sizes.sum())
+    items = items[order]
+    waves = max(1, min(int(num_waves), items.shape[0]))
+    return items, waves, int(split_sizes.sum())
 
 
 def make_prefill_items(
@@ -530,13 +552,15 @@ class MI355XAttentionBackendMixin:
 
         decode_items = None
         num_decode_items = 0
+        num_decode_waves = 0
         num_part_slots = 0
-        chunk_pages = 0
         if common.num_decode_seqs:
-            decode_counts = counts[common.num_prefill_seqs:]
-            chunk_pages = choose_decode_chunk_pages(int(decode_counts.sum()), self.num_kv_heads)
-            items, num_part_slots = make_decode_items(
-                decode_counts, common.num_prefill_seqs, common.num_prefill_tokens, chunk_pages
+            items, num_decode_waves, num_part_slots = make_decode_plan(
+                counts[common.num_prefill_seqs:],
+                common.num_prefill_seqs,
+                common.num_prefill_tokens,
+                self.num_kv_heads,
+                resident_decode_waves(block_tables.device),
             )
             num_decode_items = items.shape[0]
             decode_items = _to_device(items, block_tables.device)
@@ -569,8 +593,8 @@ class MI355XAttentionBackendMixin:
             num_prefill_pages=num_prefill_pages,
             decode_items=decode_items,
             num_decode_items=num_decode_items,
+            num_decode_waves=num_decode_waves,
             num_decode_part_slots=num_part_slots,
-            decode_chunk_pages=chunk_pages,
             prefill_items=prefill_items,
             num_prefill_items=num_prefill_items,
         )
@@ -711,6 +735,7 @@ class MI355XAttentionBackendMixin:
             metadata.seq_lens,
             metadata.decode_items,
             metadata.num_decode_items,
+            metadata.num_decode_waves,
             common.num_seqs,
             metadata.num_decode_part_slots,
             output,
@@ -749,6 +774,7 @@ class MI355XAttentionBackendMixin:
             metadata.num_prefill_items,
             metadata.decode_items,
             metadata.num_decode_items,
+            metadata.num_decode_waves,
             common.num_seqs,
             metadata.num_decode_part_slots,
             output,
@@ -875,7 +901,7 @@ __all__ = [
     "MI355XAttentionBackendMixin",
     "MI355XAttentionMetadata",
     "MI355XSplitAttentionBackend",
-    "choose_decode_chunk_pages",
-    "make_decode_items",
+    "make_decode_plan",
     "make_prefill_items",
+    "resident_decode_waves",
 ]

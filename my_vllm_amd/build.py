@@ -25,7 +25,10 @@ LIB_PATH = LIB_DIR / "libmy_vllm_amd.so"
 BUILD_DIR = PACKAGE_DIR / "_build"
 
 OFFLOAD_ARCH = "gfx950"
-# Packed fp32 VALU forms are disabled for every kernel of this library.
+# Packed fp32 VALU forms are disabled for every kernel of this library.  The
+# atomic optimizer is off: it turns a single-lane atomic into a wave-wide
+# reduction whose result is broadcast right after the atomic, which makes the
+# decode kernel's piece claims wait for every load in flight.
 HIP_FLAGS = (
     f"--offload-arch={OFFLOAD_ARCH}",
     "-O3",
@@ -38,6 +41,8 @@ HIP_FLAGS = (
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    "-mllvm",
+    "-amdgpu-atomic-optimizer-strategy=None",
 )
 
 

@@ -18,6 +18,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -28,10 +29,17 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 template <typename T>
 struct Elem;
 
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
 template <>
 struct Elem<__bf16> {
   typedef bf16x8 v8;
   typedef bf16x4 v4;
+  // 16x16x16 (K = 16): A/B hold 4 elements per lane (k = 4*(lane/16) + s).
+  __device__ static inline f32x4 mfma16k16(v4 a, v4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a),
+                                                     __builtin_bit_cast(s16x4_t, b), c, 0, 0, 0);
+  }
   __device__ static inline f32x4 mfma16(v8 a, v8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
@@ -44,6 +52,9 @@ template <>
 struct Elem<_Float16> {
   typedef f16x8 v8;
   typedef f16x4 v4;
+  __device__ static inline f32x4 mfma16k16(v4 a, v4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
   __device__ static inline f32x4 mfma16(v8 a, v8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
@@ -87,9 +98,43 @@ __device__ inline s16x4 lds_ld_tr16(const lds_u8* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
 }
 
+// Eight ds_read_b64_tr_b16 at byte offsets base + 512*i (i = 0..7), then
+// lgkmcnt(0).  Issued as one asm block: the compiler cannot see that these
+// reads do not alias in-flight global_load_lds writes to another LDS buffer
+// and would otherwise wait for every outstanding DMA before each read.
+// Callers order the block after the waits that make `base` valid.
+__device__ inline void lds_ld_tr16_x8_stride512(const lds_u8* base, s16x4 (&out)[8]) {
+  const uint32_t a = (uint32_t)(uintptr_t)base;
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %8\n"
+      "ds_read_b64_tr_b16 %1, %8 offset:512\n"
+      "ds_read_b64_tr_b16 %2, %8 offset:1024\n"
+      "ds_read_b64_tr_b16 %3, %8 offset:1536\n"
+      "ds_read_b64_tr_b16 %4, %8 offset:2048\n"
+      "ds_read_b64_tr_b16 %5, %8 offset:2560\n"
+      "ds_read_b64_tr_b16 %6, %8 offset:3072\n"
+      "ds_read_b64_tr_b16 %7, %8 offset:3584\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(out[0]), "=&v"(out[1]), "=&v"(out[2]), "=&v"(out[3]), "=&v"(out[4]), "=&v"(out[5]),
+        "=&v"(out[6]), "=&v"(out[7])
+      : "v"(a)
+      : "memory");
+}
+
 // 16-byte global -> LDS copy; lane i's bytes land at lds_base + 16*i.
 __device__ inline void dma16(const void* g, lds_u8* lds_base) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+}
+
+// As dma16, with cache-policy bits `Policy` (e.g. device-scope coherence).
+template <int Policy>
+__device__ inline void dma16_policy(const void* g, lds_u8* lds_base) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_base, 16, 0, Policy);
+}
+
+template <typename V>
+__device__ inline V lds_ld8(const lds_u8* p) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) V*>(p);
 }
 
 // Compiler-level ordering point for LDS traffic that is shared between lanes

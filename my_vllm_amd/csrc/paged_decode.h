@@ -1,4 +1,5 @@
-// Paged GQA decode: one wavefront per (sequence chunk, KV head) work item.
+// Paged GQA decode on gfx950: a persistent grid of wavefronts, each streaming
+// an equal share of the batch's (sequence, KV head, page) units.
 //
 // Replaces FlashInfer's BatchDecodeWithPagedKVCacheWrapper.run on the DECODE
 // route of the reference backend (nanovllm/layers/attention_backend.py:995-997)
@@ -6,23 +7,38 @@
 //   o = sum_j softmax_j(scale * q . K[j]) V[j]   over j < seq_len,
 // with K/V gathered from NHD pages [P, 16, Hkv, D] through block_tables.
 //
-// Layout of the work (one 64-lane wavefront per item):
-//  * The G query heads that share a KV head form the N=16 side of the
-//    16x16x32 MFMA (rows >= G are zero), so every K/V byte read from HBM serves
-//    all G heads: S^T[token, g] = K[token, :] . Q[g, :].
-//  * A tile is 2 pages (32 tokens).  K goes straight from HBM into MFMA
-//    A-operand registers (lane = token, 16-byte d-chunks).  V goes from HBM
-//    straight into LDS (global_load_lds, row-major, XOR-swizzled 16-byte
-//    chunks, double-buffered) and is read back transposed with
-//    ds_read_b64_tr_b16 as the A operand of O^T[d, g] += V^T[d, t] P^T[t, g];
-//    the C layout of S^T is already the B-operand layout of P^T.
+// Work distribution: the host cuts every (sequence, KV head) into pieces of a
+// few pages (longest first); about one wavefront per resident wave slot is
+// launched.  Wavefront w starts on piece w and then takes pieces from a
+// device-scope counter, so CUs that get more HBM bandwidth simply process
+// more pieces (per-CU bandwidth on a multi-XCD part is uneven enough that an
+// equal static split ends up waiting for the slowest CU).  The next piece's
+// index is claimed one piece ahead and its page table and queries are loaded
+// while the current piece streams, so its first page is in flight before the
+// current piece's epilogue runs.  The last wavefront to exit resets the
+// counters for the next launch.
+//
+// Inside a wavefront:
+//  * The G query heads that share a KV head form the N=16 side of the MFMAs
+//    (columns >= G are zero), so every K/V byte read from HBM serves all G
+//    heads: S^T[token, g] = K[token, :] . Q[g, :].
+//  * A tile is one 16-token page of one KV head (4 KB of K, 4 KB of V).  Both
+//    go from HBM straight into LDS with global_load_lds (16 bytes per lane,
+//    no registers), double-buffered, so a wavefront never carries pending
+//    loads in registers.
+//  * S^T (16x16x32 MFMA): A = K fragments read from a chunk-major LDS page
+//    (lane = token), B = Q held in registers.  PV (16x16x16 MFMA):
+//    O^T[d, g] += V^T[d, t] P^T[t, g], A = V^T read with ds_read_b64_tr_b16
+//    from a chunk-major LDS page; B = P^T is exactly the C layout of S^T, so
+//    no shuffle is needed.
 //  * Online softmax in the log2 domain, fp32 accumulators, P rounded to the
-//    storage type for the PV MFMA.
-//  * Long contexts are split into chunks (split-K).  Each chunk writes an fp32
-//    partial (o / l, log2-sum-exp); the last chunk of a (sequence, KV head) to
-//    finish, detected with a device-scope counter, merges the partials, so one
-//    launch produces the final output.  Counters are reset by the merger, so
-//    the workspace only has to be zeroed when first allocated.
+//    storage type for the PV MFMA; the O rescale is skipped unless the
+//    running max grows by more than 8 (log2 units).
+//  * A (sequence, KV head) split into several pieces (split-K) gets one fp32
+//    partial per piece (o / l, log2-sum-exp); the last piece to finish,
+//    detected with a device-scope counter, merges the partials, so one launch
+//    produces the final output.  Counters are reset by the merger, so the
+//    workspace only has to be zeroed when first allocated.
 #pragma once
 
 #include "mva_common.h"
@@ -33,20 +49,17 @@ namespace mva {
 
 constexpr int kHeadDim = 128;
 constexpr int kPageSize = 16;
-// Bytes of one LDS V buffer of decode_item (two 16-token pages); decode_item
-// takes two such buffers (double buffering), which should be distinct
-// __shared__ arrays so the compiler can tell their LDS-DMA writes apart.
-constexpr int kDecodeVBufBytes = 2 * kPageSize * kHeadDim * 2;
-// Longest chunk (pages) one decode work item may cover.
-constexpr int kMaxChunkPages = 128;
-// int32 fields per decode work item (see make_decode_items on the host).
+// One page of one KV head (K or V) in LDS, and the LDS a decode wavefront
+// uses: two buffers of (K page, V page).
+constexpr int kDecodePageBytes = kPageSize * kHeadDim * 2;
+constexpr int kDecodeWaveLdsBytes = 2 * 2 * kDecodePageBytes;
+// int32 fields per decode work item (piece), see make_decode_plan on the host:
+// {seq, page_begin, page_end, chunk, n_chunks, part_base, q_row, kv_head}.
 constexpr int kDecodeItemInts = 8;
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt bits [3:0] and [15:14], expcnt
 // [6:4], lgkmcnt [11:8]); only vmcnt is constrained.
 constexpr int waitcnt_vm(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
-// One tile issues 16 vector-memory instructions (8 K loads, 8 V LDS loads).
-constexpr int kVmcntTile = waitcnt_vm(16);
 constexpr int kVmcnt0 = waitcnt_vm(0);
 
 struct DecodeParams {
@@ -61,8 +74,10 @@ struct DecodeParams {
   const int32_t* block_tables;
   int64_t bt_stride;
   const int32_t* seq_lens;
-  const int32_t* items;  // [num_items][8]: seq, page_begin, page_end, chunk, n_chunks, part_base, q_row, 0
+  const int32_t* items;  // [num_items][8], see kDecodeItemInts
   int num_items;
+  int num_waves;  // wavefronts in the launch
+  int32_t* sched;  // claim counters and exit counter, see kDecodeClaimCounters
   void* out;
   int64_t out_tok_stride;
   int64_t out_head_stride;
@@ -74,12 +89,6 @@ struct DecodeParams {
   float scale_log2;
 };
 
-template <typename T>
-struct DecodeTile {
-  typedef typename Elem<T>::v8 V8;
-  V8 k[2][4];  // k[pp][j] = K[page pp][token c][32*q4 + 8*j .. +8]
-};
-
 __device__ inline float wave_max16(float x) {
   x = fmaxf(x, __shfl_xor(x, 16));
   return fmaxf(x, __shfl_xor(x, 32));
@@ -89,267 +98,649 @@ __device__ inline float wave_sum16(float x) {
   return x + __shfl_xor(x, 32);
 }
 
-// Swizzled byte offset of 16-byte chunk `ch` of token row `t` in a V page
-// staged in LDS: rows are 256 bytes, chunks are XOR-ed with 2*(t & 7) so that
-// the transposed reads of 16 token rows hit distinct banks.
-__device__ inline int vlds_off(int t, int ch) { return t * 256 + ((ch ^ ((t & 7) << 1)) << 4); }
-
-// Issues the loads of one tile (pages `page0`, `page1`): K into MFMA A-operand
-// registers and V straight from HBM into LDS (gfx950 global_load_lds, 16 bytes
-// per lane, no registers), laid out by vlds_off.  Instruction i of page pp
-// fills LDS bytes [pp*4096 + 1024*i, +1024): token row 4*i + lane/16, physical
-// chunk lane%16.  16 vector-memory instructions per tile.
 template <typename T>
-__device__ inline void decode_load_tile(const DecodeParams& p, const T* kc, const T* vc, int page0,
-                                        int page1, int lane, DecodeTile<T>& tile, lds_u8* vlds) {
-  typedef typename Elem<T>::v8 V8;
-  const int q4 = lane >> 4;
-  const int c = lane & 15;
-#pragma unroll
-  for (int pp = 0; pp < 2; ++pp) {
-    const int page = pp ? page1 : page0;
-    const T* kp = kc + (int64_t)page * p.page_stride;
-    const T* vp = vc + (int64_t)page * p.page_stride;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = 4 * i + q4;
-      const int ch = c ^ ((t & 7) << 1);
-      dma16(vp + t * p.tok_stride + 8 * ch, vlds + pp * 4096 + 1024 * i);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) tile.k[pp][j] = ld16<V8>(kp + c * p.tok_stride + 32 * q4 + 8 * j);
+__device__ inline void merge_partials(const DecodeParams& p, int s, int h, int pbase, int nchunks,
+                                      int64_t qrow, int lane, lds_u8* scratch);
+
+// Scalar (SMEM) loads of data that is read-only for the whole launch (work
+// lists, page tables, lengths).  The constant address space tells the
+// compiler the memory is invariant, so a wave-uniform index becomes an
+// s_load whose completion is tracked by lgkmcnt, independent of the page
+// DMAs counted by vmcnt.
+typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(4))) const int32_t const_i32;
+typedef __attribute__((address_space(4))) const i32x8 const_i32x8;
+
+__device__ inline int sload(const int32_t* base, int64_t idx) { return ((const_i32*)base)[idx]; }
+
+// ---- vector-memory operations the compiler does not track -----------------
+// Once a store or a returning atomic is outstanding, the compiler's wait
+// insertion assumes vector-memory operations may complete out of order and
+// waits for all of them (vmcnt(0)) before any later load result is used,
+// which would drain the page stream at every piece boundary.  On this GPU
+// vector-memory operations report completion in issue order, so the decode
+// loop issues its atomics, stores and per-piece loads as inline asm (not
+// counted by the compiler) and orders their completion itself.  Every
+// operation whose result is read is issued in the same asm statement as the
+// wait that retires it (decode_step), so no compiler-generated instruction
+// can touch a destination register while the operation is in flight.
+
+// Per-iteration memory work of a decode wavefront, issued as one asm
+// statement, in this order:
+//   * lane 0: claim = atomic_add(claim_ptr, 1) if `claiming`;
+//   * lane 0: arrival = atomic_add(arrive_ptr, 1) if `arriving`;
+//   * all lanes, if `claiming`: the next piece's page-table words
+//     (bt0 -> bt_lo, bt1 -> bt_hi) and query fragments (q .. q + 63 -> qv);
+//   * if kDma: the 8 DMAs of one page of one KV head (4 to lds_v, 4 to
+//     lds_k, 1 KB each), then s_waitcnt vmcnt(8), which retires everything
+//     above and the previous page; otherwise s_waitcnt vmcnt(0).
+// Page layout in LDS: K at lds_k and V at lds_v are both chunk-major (byte
+// chunk*256 + token*16).  DMA i reads, per lane, 16 bytes at v_src/k_src +
+// 64*i, where the caller's lane address is token lane%16, d-chunk lane/16,
+// so DMA i holds d-chunks 4i..4i+3 of all 16 tokens.  The K A-operand read
+// (16 tokens at one chunk) and the V transposed read (4 tokens x 2 chunks
+// per 16-lane group) both cover whole 256-byte bank rows.
+// `claiming` and `arriving` are wave-uniform.  Outputs not issued keep their
+// previous contents (claim/arrival: unspecified).
+struct DecodeStepIo {
+  int claim;
+  int arrival;
+  int bt_lo;
+  int bt_hi;
+  u32x4 qv[4];
+};
+
+template <bool kDma>
+__device__ inline void decode_step(DecodeStepIo& io, int claiming, int arriving, int* claim_ptr, int* arrive_ptr,
+                                   const int32_t* bt0, const int32_t* bt1, const void* q, const void* v_src,
+                                   const void* k_src, uint32_t lds_v, uint32_t lds_k) {
+  uint64_t saved;
+  uint32_t m0_saved;
+  const int on_c = __builtin_amdgcn_readfirstlane(claiming != 0 ? 1 : 0);
+  const int on_a = __builtin_amdgcn_readfirstlane(arriving != 0 ? 1 : 0);
+  lds_v = __builtin_amdgcn_readfirstlane(lds_v);
+  lds_k = __builtin_amdgcn_readfirstlane(lds_k);
+  const char* v = (const char*)v_src;
+  const char* k = (const char*)k_src;
+  if constexpr (kDma) {
+    asm volatile(
+        "s_mov_b64 %[sv], exec\n\t"
+        "s_mov_b32 exec_lo, %[onc]\n\t"
+        "s_mov_b32 exec_hi, 0\n\t"
+        "global_atomic_add %[cl], %[cp], %[one], off sc0\n\t"
+        "s_mov_b32 exec_lo, %[ona]\n\t"
+        "global_atomic_add %[ar], %[ap], %[one], off sc0\n\t"
+        "s_cmp_eq_u32 %[onc], 0\n\t"
+        "s_cselect_b64 exec, 0, %[sv]\n\t"
+        "global_load_dword %[blo], %[b0], off\n\t"
+        "global_load_dword %[bhi], %[b1], off\n\t"
+        "global_load_dwordx4 %[q0], %[qp], off\n\t"
+        "global_load_dwordx4 %[q1], %[qp], off offset:16\n\t"
+        "global_load_dwordx4 %[q2], %[qp], off offset:32\n\t"
+        "global_load_dwordx4 %[q3], %[qp], off offset:48\n\t"
+        "s_mov_b64 exec, %[sv]\n\t"
+        "s_mov_b32 %[m0s], m0\n\t"
+        "s_mov_b32 m0, %[lv]\n\t"
+        "global_load_lds_dwordx4 %[v0], off\n\t"
+        "s_add_u32 m0, %[lv], 0x400\n\t"
+        "global_load_lds_dwordx4 %[v1], off\n\t"
+        "s_add_u32 m0, %[lv], 0x800\n\t"
+        "global_load_lds_dwordx4 %[v2], off\n\t"
+        "s_add_u32 m0, %[lv], 0xc00\n\t"
+        "global_load_lds_dwordx4 %[v3], off\n\t"
+        "s_mov_b32 m0, %[lk]\n\t"
+        "global_load_lds_dwordx4 %[k0], off\n\t"
+        "s_add_u32 m0, %[lk], 0x400\n\t"
+        "global_load_lds_dwordx4 %[k1], off\n\t"
+        "s_add_u32 m0, %[lk], 0x800\n\t"
+        "global_load_lds_dwordx4 %[k2], off\n\t"
+        "s_add_u32 m0, %[lk], 0xc00\n\t"
+        "global_load_lds_dwordx4 %[k3], off\n\t"
+        "s_mov_b32 m0, %[m0s]\n\t"
+        "s_waitcnt vmcnt(8)"
+        : [cl] "=&v"(io.claim), [ar] "=&v"(io.arrival), [blo] "+v"(io.bt_lo), [bhi] "+v"(io.bt_hi),
+          [q0] "+v"(io.qv[0]), [q1] "+v"(io.qv[1]), [q2] "+v"(io.qv[2]), [q3] "+v"(io.qv[3]), [sv] "=&s"(saved),
+          [m0s] "=&s"(m0_saved)
+        : [onc] "s"(on_c), [ona] "s"(on_a), [cp] "v"(claim_ptr), [ap] "v"(arrive_ptr), [one] "v"(1),
+          [b0] "v"(bt0), [b1] "v"(bt1), [qp] "v"(q), [lv] "s"(lds_v), [lk] "s"(lds_k), [v0] "v"(v),
+          [v1] "v"(v + 64), [v2] "v"(v + 128), [v3] "v"(v + 192), [k0] "v"(k), [k1] "v"(k + 64),
+          [k2] "v"(k + 128), [k3] "v"(k + 192)
+        : "memory", "scc");
+  } else {
+    asm volatile(
+        "s_mov_b64 %[sv], exec\n\t"
+        "s_mov_b32 exec_lo, %[onc]\n\t"
+        "s_mov_b32 exec_hi, 0\n\t"
+        "global_atomic_add %[cl], %[cp], %[one], off sc0\n\t"
+        "s_mov_b32 exec_lo, %[ona]\n\t"
+        "global_atomic_add %[ar], %[ap], %[one], off sc0\n\t"
+        "s_cmp_eq_u32 %[onc], 0\n\t"
+        "s_cselect_b64 exec, 0, %[sv]\n\t"
+        "global_load_dword %[blo], %[b0], off\n\t"
+        "global_load_dword %[bhi], %[b1], off\n\t"
+        "global_load_dwordx4 %[q0], %[qp], off\n\t"
+        "global_load_dwordx4 %[q1], %[qp], off offset:16\n\t"
+        "global_load_dwordx4 %[q2], %[qp], off offset:32\n\t"
+        "global_load_dwordx4 %[q3], %[qp], off offset:48\n\t"
+        "s_mov_b64 exec, %[sv]\n\t"
+        "s_waitcnt vmcnt(0)"
+        : [cl] "=&v"(io.claim), [ar] "=&v"(io.arrival), [blo] "+v"(io.bt_lo), [bhi] "+v"(io.bt_hi),
+          [q0] "+v"(io.qv[0]), [q1] "+v"(io.qv[1]), [q2] "+v"(io.qv[2]), [q3] "+v"(io.qv[3]), [sv] "=&s"(saved)
+        : [onc] "s"(on_c), [ona] "s"(on_a), [cp] "v"(claim_ptr), [ap] "v"(arrive_ptr), [one] "v"(1),
+          [b0] "v"(bt0), [b1] "v"(bt1), [qp] "v"(q)
+        : "memory", "scc");
   }
 }
 
+// Device-scope (write-through) stores, and a plain 8-byte store.  The
+// trailing s_nop covers the store-data hazard for multi-dword stores.
+__device__ inline void store16_device_untracked(void* addr, u32x4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(addr), "v"(v) : "memory");
+}
+__device__ inline void store4_device_untracked(void* addr, float v) {
+  asm volatile("global_store_dword %0, %1, off sc1" ::"v"(addr), "v"(v) : "memory");
+}
+__device__ inline void store8_untracked(void* addr, u32x2 v) {
+  asm volatile("global_store_dwordx2 %0, %1, off\n\ts_nop 1" ::"v"(addr), "v"(v) : "memory");
+}
+
+// Piece claim counters: kDecodeClaimCounters counters, each on its own
+// 128-byte line (atomics to one line serialize), then the exit counter.
+constexpr int kDecodeClaimCounters = 32;
+constexpr int kDecodeSchedLineInts = 32;
+constexpr int kDecodeSchedBytes = 4352;  // (32 + 1) lines of 128 bytes, rounded up to 256
+static_assert((kDecodeClaimCounters + 1) * kDecodeSchedLineInts * 4 <= kDecodeSchedBytes, "sched area");
+
+// One wavefront of a decode launch (`wave` in [0, num_waves)); `lds` is its
+// kDecodeWaveLdsBytes of LDS.
+//
+// Piece order: wavefront w takes piece w, then piece W + w (W = num_waves),
+// then pieces 2W + C*k + (w mod C) for k drawn from claim counter (w mod C),
+// C = min(32, W).  Three pieces are tracked: X (being computed), Y (its
+// successor: descriptor and length known, page table and queries loaded
+// during X's first page) and Z (Y's successor, claimed at X's first page;
+// its descriptor is fetched right after that page).  The page stream runs
+// one page ahead across piece boundaries, so the first page of Y (or of Z,
+// when Y is a single page) is in flight while X's last page is computed,
+// and a piece boundary costs no wait of its own.  Page ids come from the
+// page-table registers (readlane); the loop issues no memory access per
+// page other than the page itself.
+//
+// Split-K arrivals: a split piece stores its partial when it ends (iteration
+// k); the stores are complete after the wait of iteration k+1, so the
+// arrival counter is incremented at the top of iteration k+2 and examined
+// after that iteration's wait.  The last arrival merges, in the same
+// iteration, after the page is computed (that page buffer is then free).
 template <typename T>
-__device__ void decode_item(const DecodeParams& p, const int32_t* __restrict__ it, int h,
-                            lds_u8* vbuf0, lds_u8* vbuf1) {
+__device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
   typedef typename Elem<T>::v8 V8;
+  typedef typename Elem<T>::v4 V4;
   const int lane = threadIdx.x & 63;
   const int q4 = lane >> 4;
   const int c = lane & 15;
-  const int s = it[0], pb = it[1], pe = it[2], chunk = it[3], nchunks = it[4], pbase = it[5];
-  const int64_t qrow = it[6];
   const int G = p.group;
-  const int seq_len = p.seq_lens[s];
-  const T* kc = (const T*)p.k_cache + h * kHeadDim;
-  const T* vc = (const T*)p.v_cache + h * kHeadDim;
-  const int32_t* bt = p.block_tables + (int64_t)s * p.bt_stride;
+  const int Hkv = p.num_kv_heads;
+  const int W = p.num_waves;
+  const int N = p.num_items;
+  const int C = min(kDecodeClaimCounters, W);
+  const bool q_lane = c < G;
+  int* const claim_ctr = p.sched + (wave % C) * kDecodeSchedLineInts;
 
-  // Q as the B operand of S^T = K Q^T: lane (q4, c) holds Q[g = c][32*q4 + 8*j .. +8].
-  V8 qf[4];
-  if (c < G) {
-    const T* qp = (const T*)p.q + qrow * p.q_tok_stride + (int64_t)(h * G + c) * p.q_head_stride + 32 * q4;
+  // Descriptor fields: {seq, page_begin, page_end, chunk, n_chunks, part_base, q_row, kv_head}.
+  auto desc_at = [&](int idx) -> i32x8 { return ((const_i32x8*)p.items)[idx]; };
+  // Page table of piece d (at most 128 pages): lane L of lo/hi holds page L
+  // and 64 + L; bt_word gives the clamped address of word k.
+  auto bt_word = [&](const i32x8& d, int k) -> const int32_t* {
+    return p.block_tables + (int64_t)d[0] * p.bt_stride + d[1] + min(k, d[2] - d[1] - 1);
+  };
+  auto page_of = [&](int lo, int hi, int k) -> int {
+    const int a = __builtin_amdgcn_readlane(lo, k & 63);
+    const int b = __builtin_amdgcn_readlane(hi, k & 63);
+    const int pg = k < 64 ? a : b;
+    return (pg >= 0 && pg < p.num_pages) ? pg : 0;
+  };
+  // Query fragments of piece d, the B operand of S^T = K Q^T: lane (q4, c)
+  // holds Q[g = c][32*q4 + 8*j .. +8].  Lanes c >= G read head 0 of the
+  // group (in bounds) and are zeroed where the fragments are used.
+  auto q_addr = [&](const i32x8& d) -> const T* {
+    const int g = q_lane ? c : 0;
+    return (const T*)p.q + (int64_t)d[6] * p.q_tok_stride + (int64_t)(d[7] * G + g) * p.q_head_stride + 32 * q4;
+  };
+
+  // ---- piece state --------------------------------------------------------
+  i32x8 X = desc_at(wave);
+  int yi = wave + W;  // >= N: none
+  int zi = N;
+  i32x8 Y = X, Z = X;
+  if (yi < N) Y = desc_at(yi);
+  int seq_len = sload(p.seq_lens, X[0]);
+  int y_len = sload(p.seq_lens, Y[0]);
+  int z_len = 0;
+  int np = X[2] - X[1];
+  // X's page table and queries; the first DMA needs the table, so this is
+  // the one wait of the wavefront outside the page loop.
+  int bt_lo = *bt_word(X, lane), bt_hi = *bt_word(X, 64 + lane);
+  u32x4 qf[4];
+  {
+    const T* qp = q_addr(X);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) qf[j] = ld16<V8>(qp + 8 * j);
-  } else {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) qf[j] = V8{};
+    for (int j = 0; j < 4; ++j) qf[j] = ld16<u32x4>(qp + 8 * j);
   }
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);
+  DecodeStepIo io;
+  io.bt_lo = io.bt_hi = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) io.qv[j] = u32x4{0u, 0u, 0u, 0u};
+
+  // Split-K pieces whose partial stores are in flight (arrival counter
+  // offset and piece index; index -1: none): `a` was stored two iterations
+  // back (its arrival is due at the next loop top), `b` in the previous one.
+  int a_ctr = 0, a_idx = -1, a_n = 0, b_ctr = 0, b_idx = -1, b_n = 0;
+  int xi = wave;
 
   f32x4 o[8];  // o[mt][r] = O^T[d = 16*mt + 4*q4 + r][g = c]
 #pragma unroll
   for (int mt = 0; mt < 8; ++mt) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY;  // running max of scaled scores (log2 domain), per g = c
+  float m = -INFINITY;  // reference max of scaled scores (log2 domain), per g = c
   float l = 0.f;        // this lane's share of the running denominator
 
-  const int ntiles = (pe - pb + 1) >> 1;
-  // Transposed V^T reads: lane c of group q4 supplies token row 4*q4 + c/4 at
-  // d offset 4*(c%4) of each 16-wide d block and receives V[4*q4 + e][16*mt + c].
-  const int tt = 4 * q4 + (c >> 2);
-  const int dsub = (c & 3) * 4;
+  // Per-lane LDS offsets: K fragment (token c, chunk 4*q4 + j: byte
+  // (4*q4 + j)*256 + 16*c), and the transposed V read: lane c of group q4
+  // supplies token 4*q4 + c/4 at d 16*mt + 4*(c%4) (chunk 2*mt + (c%4)/2,
+  // byte 8*(c%2) inside it) and receives V[4*q4 + e][16*mt + c], e = 0..3.
+  const int koff = q4 * 1024 + c * 16;
+  const int voff = kDecodePageBytes + ((c >> 1) & 1) * 256 + (4 * q4 + (c >> 2)) * 16 + (c & 1) * 8;
 
-  // `edge` tiles contain masked tokens (sequence end, or an odd page past the
-  // chunk end); the choice is wave-uniform and made per tile by `run`.
-  auto compute = [&](int t, const DecodeTile<T>& tile, const lds_u8* vbuf, auto edge_tag) {
+  // `edge` pages contain tokens past seq_len; the choice is wave-uniform.
+  auto compute = [&](int pg, const lds_u8* buf, auto edge_tag) {
     constexpr bool edge = decltype(edge_tag)::value;
-    const int pg0 = pb + 2 * t;
-    f32x4 sc[2];
+    f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int pp = 0; pp < 2; ++pp) {
-      sc[pp] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sc[pp] = Elem<T>::mfma16(tile.k[pp][j], qf[j], sc[pp]);
-    }
-    float x[2][4];
+    for (int j = 0; j < 4; ++j)
+      sc = Elem<T>::mfma16(lds_ld16<V8>(buf + koff + j * 256), q_lane ? __builtin_bit_cast(V8, qf[j]) : V8{}, sc);
+    // sc[r] = S[token 4*q4 + r][g = c]
     float tmax = -INFINITY;
 #pragma unroll
-    for (int pp = 0; pp < 2; ++pp) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        x[pp][r] = sc[pp][r] * p.scale_log2;
-        if constexpr (edge) {
-          const int pos = (pg0 + pp) * kPageSize + 4 * q4 + r;
-          if ((pg0 + pp) >= pe || pos >= seq_len) x[pp][r] = -INFINITY;
-        }
-        tmax = fmaxf(tmax, x[pp][r]);
+    for (int r = 0; r < 4; ++r) {
+      if constexpr (edge) {
+        if (pg * kPageSize + 4 * q4 + r >= seq_len) sc[r] = -INFINITY;
       }
+      tmax = fmaxf(tmax, sc[r]);
     }
-    tmax = wave_max16(tmax);
-    const float m_new = fmaxf(m, tmax);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = fast_exp2(m - m_use);
-    m = m_new;
-    V8 pf;
-    float psum = 0.f;
+    tmax = wave_max16(tmax) * p.scale_log2;  // scale > 0 commutes with max
+    // Move the reference max only when it grows by > 8 (p stays <= 2^8).
+    const bool grow = tmax > m + 8.0f;
+    if (__any(grow)) {
+      const float m_new = grow ? tmax : m;
+      const float alpha = grow ? fast_exp2(m - m_new) : 1.0f;  // m = -inf -> 0
+      m = m_new;
+      l *= alpha;
 #pragma unroll
-    for (int pp = 0; pp < 2; ++pp) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float pr = fast_exp2(x[pp][r] - m_use);
-        psum += pr;
-        pf[pp * 4 + r] = (T)pr;
-      }
+      for (int mt = 0; mt < 8; ++mt) o[mt] *= alpha;
     }
-    l = l * alpha + psum;
+    const float m_use = (m == -INFINITY) ? 0.f : m;
+    V4 pf;
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt) o[mt] *= alpha;
-
-    // Element e of the page-pp half of a V^T fragment is token 4*q4 + e.
-    unsigned vmask = 0xffu;  // bit pp*4+e set = token valid
-    if constexpr (edge) {
-      vmask = 0;
-#pragma unroll
-      for (int pp = 0; pp < 2; ++pp)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int pos = (pg0 + pp) * kPageSize + 4 * q4 + e;
-          if ((pg0 + pp) < pe && pos < seq_len) vmask |= 1u << (pp * 4 + e);
-        }
+    for (int r = 0; r < 4; ++r) {
+      const float pr = fast_exp2(sc[r] * p.scale_log2 - m_use);
+      l += pr;
+      pf[r] = (T)pr;
     }
+    s16x4 vt[8];
+    lds_ld_tr16_x8_stride512(buf + voff, vt);
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
-      const int d = 16 * mt + dsub;
-      const int off = vlds_off(tt, d >> 3) + (d & 7) * 2;
-      const s16x4 lo = lds_ld_tr16(vbuf + off);
-      const s16x4 hi = lds_ld_tr16(vbuf + 4096 + off);
-      s16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      s16x4 v = vt[mt];
       if constexpr (edge) {
-        // Zero V of masked tokens so stale (possibly NaN) cache rows cannot
-        // leak through 0 * NaN in the PV product.
+        // Zero V of tokens past seq_len: stale (possibly NaN) cache rows
+        // must not leak through 0 * NaN in the PV product.
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (!((vmask >> e) & 1u)) both[e] = 0;
+        for (int e = 0; e < 4; ++e)
+          if (pg * kPageSize + 4 * q4 + e >= seq_len) v[e] = 0;
       }
-      o[mt] = Elem<T>::mfma16(__builtin_bit_cast(V8, both), pf, o[mt]);
+      o[mt] = Elem<T>::mfma16k16(__builtin_bit_cast(V4, v), pf, o[mt]);
     }
   };
 
-  // The chunk's page table lives in two VGPRs (lane i: pages i and 64 + i of
-  // the chunk; chunks are at most kMaxChunkPages long) and is read with
-  // v_readlane, so the tile loop issues no dependent memory reads.
-  const int np = pe - pb;
-  const int bt_lo = lane < np ? bt[pb + lane] : 0;
-  const int bt_hi = lane + 64 < np ? bt[pb + 64 + lane] : 0;
-  auto page_at = [&](int k) -> int {
-    const int a = __builtin_amdgcn_readlane(bt_lo, k & 63);
-    const int b = __builtin_amdgcn_readlane(bt_hi, k & 63);
-    const int pg = k < 64 ? a : b;
-    return (pg >= 0 && pg < p.num_pages) ? pg : 0;
-  };
-  // Tile t covers chunk pages 2t and 2t+1; a missing odd page and the
-  // prefetch past the last tile re-read pages already in flight (cache hits)
-  // and are masked or ignored, so every iteration issues the same loads.
-  auto load = [&](int t, DecodeTile<T>& tile, lds_u8* vbuf) {
-    t = t < ntiles ? t : ntiles - 1;
-    const int k0 = 2 * t;
-    const int k1 = (2 * t + 1 < np) ? 2 * t + 1 : 2 * t;
-    decode_load_tile<T>(p, kc, vc, page_at(k0), page_at(k1), lane, tile, vbuf);
-  };
-  auto run = [&](int t, const DecodeTile<T>& tile, const lds_u8* vbuf) {
-    const int pg0 = pb + 2 * t;
-    if ((pg0 + 2 > pe) || ((pg0 + 2) * kPageSize > seq_len)) compute(t, tile, vbuf, std::true_type{});
-    else compute(t, tile, vbuf, std::false_type{});
+  // End of piece X: the final output, or its split-K partial (normalised o
+  // and log2-sum-exp, device-scope stores that go past this XCD's L2).
+  auto finish_piece = [&]() {
+    const float l_tot = wave_sum16(l);
+    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    const int h = X[7];
+    if (X[4] == 1) {
+      if (q_lane) {
+        T* op = (T*)p.out + (int64_t)X[6] * p.out_tok_stride + (int64_t)(h * G + c) * p.out_head_stride + 4 * q4;
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) {
+          V4 w;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) w[r] = (T)(o[mt][r] * inv);
+          store8_untracked(op + 16 * mt, __builtin_bit_cast(u32x2, w));
+        }
+      }
+      return;
+    }
+    const int64_t slot = (int64_t)(X[5] + X[3]) * Hkv + h;
+    if (q_lane) {
+      float* po = p.part_o + (slot * G + c) * kHeadDim + 4 * q4;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) store16_device_untracked(po + 16 * mt, __builtin_bit_cast(u32x4, o[mt] * inv));
+      if (q4 == 0)
+        store4_device_untracked(&p.part_lse[slot * G + c], l_tot > 0.f ? m + fast_log2(l_tot) : -INFINITY);
+    }
   };
 
-  if (ntiles > 0) {
-    DecodeTile<T> ta, tb;
-    load(0, ta, vbuf0);
-    for (int t = 0; t < ntiles; t += 2) {
-      load(t + 1, tb, vbuf1);
-      __builtin_amdgcn_s_waitcnt(kVmcntTile);
-      wave_lds_fence();
-      run(t, ta, vbuf0);
-      wave_lds_fence();
-      load(t + 2, ta, vbuf0);
-      __builtin_amdgcn_s_waitcnt(kVmcntTile);
-      wave_lds_fence();
-      if (t + 1 < ntiles) run(t + 1, tb, vbuf1);
-      wave_lds_fence();
-    }
-    // Drain the final prefetch: LDS writes must land before the wave exits.
-    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+  // ---- page stream --------------------------------------------------------
+  // (fh, fpg) is the page the next iteration DMAs; fvalid == 0 when nothing
+  // follows.
+  {
+    // X's first page, through the same asm path as every later page (the
+    // compiler then tracks no LDS DMA at all in the loop).
+    const int64_t base = (int64_t)page_of(bt_lo, bt_hi, 0) * p.page_stride + X[7] * kHeadDim;
+    const int64_t lane_off = (lane & 15) * p.tok_stride + 8 * (lane >> 4);
+    const uint32_t lds_k = (uint32_t)(uintptr_t)lds;
+    decode_step<true>(io, 0, 0, claim_ctr, p.counters, bt_word(X, lane), bt_word(X, 64 + lane), q_addr(X),
+                      (const T*)p.v_cache + base + lane_off, (const T*)p.k_cache + base + lane_off,
+                      lds_k + kDecodePageBytes, lds_k);
+  }
+  int fvalid = 1;
+  int fh = X[7], fpg = 0;
+  if (np > 1) {
+    fpg = page_of(bt_lo, bt_hi, 1);
+  } else if (yi < N) {
+    fh = Y[7];
+    fpg = sload(p.block_tables, (int64_t)Y[0] * p.bt_stride + Y[1]);
+    fpg = (fpg >= 0 && fpg < p.num_pages) ? fpg : 0;
+  } else {
+    fvalid = 0;
   }
 
-  const float l_tot = wave_sum16(l);
-  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  int i = 0;  // page of X being computed
+  int buf = 0;
+  for (;;) {
+    // Loop state is wave-uniform; re-assert it so that the lane-dependent
+    // code in the loop does not make the compiler keep it in VGPRs.
+    i = __builtin_amdgcn_readfirstlane(i);
+    np = __builtin_amdgcn_readfirstlane(np);
+    buf = __builtin_amdgcn_readfirstlane(buf);
+    seq_len = __builtin_amdgcn_readfirstlane(seq_len);
+    y_len = __builtin_amdgcn_readfirstlane(y_len);
+    z_len = __builtin_amdgcn_readfirstlane(z_len);
+    fh = __builtin_amdgcn_readfirstlane(fh);
+    fpg = __builtin_amdgcn_readfirstlane(fpg);
+    fvalid = __builtin_amdgcn_readfirstlane(fvalid);
+    xi = __builtin_amdgcn_readfirstlane(xi);
+    yi = __builtin_amdgcn_readfirstlane(yi);
+    zi = __builtin_amdgcn_readfirstlane(zi);
+    a_ctr = __builtin_amdgcn_readfirstlane(a_ctr);
+    a_idx = __builtin_amdgcn_readfirstlane(a_idx);
+    a_n = __builtin_amdgcn_readfirstlane(a_n);
+    b_ctr = __builtin_amdgcn_readfirstlane(b_ctr);
+    b_idx = __builtin_amdgcn_readfirstlane(b_idx);
+    b_n = __builtin_amdgcn_readfirstlane(b_n);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      X[k] = __builtin_amdgcn_readfirstlane(X[k]);
+      Y[k] = __builtin_amdgcn_readfirstlane(Y[k]);
+      Z[k] = __builtin_amdgcn_readfirstlane(Z[k]);
+    }
+    lds_u8* cur = lds + buf * (2 * kDecodePageBytes);
+    lds_u8* nxt = lds + (buf ^ 1) * (2 * kDecodePageBytes);
+
+    // One asm statement issues Y's page table and queries and the claim for
+    // Z (first page of X), the arrival of the split piece whose stores the
+    // previous wait completed, and the next page's DMAs, then waits for all
+    // of it but those DMAs (see decode_step).
+    const int claiming = (i == 0 && yi < N) ? 1 : 0;
+    const int arriving = a_idx >= 0 ? 1 : 0;
+    const int d_idx = a_idx;
+    const int d_n = a_n;
+    if (fvalid) {
+      const int64_t base = (int64_t)fpg * p.page_stride + fh * kHeadDim;
+      const int64_t lane_off = (lane & 15) * p.tok_stride + 8 * (lane >> 4);
+      const uint32_t lds_k = (uint32_t)(uintptr_t)nxt;
+      decode_step<true>(io, claiming, arriving, claim_ctr, p.counters + a_ctr, bt_word(Y, lane), bt_word(Y, 64 + lane),
+                        q_addr(Y), (const T*)p.v_cache + base + lane_off, (const T*)p.k_cache + base + lane_off,
+                        lds_k + kDecodePageBytes, lds_k);
+    } else {
+      decode_step<false>(io, claiming, arriving, claim_ctr, p.counters + a_ctr, bt_word(Y, lane),
+                         bt_word(Y, 64 + lane), q_addr(Y), nullptr, nullptr, 0, 0);
+    }
+    wave_lds_fence();
+    a_ctr = b_ctr;
+    a_idx = b_idx;
+    a_n = b_n;
+    b_idx = -1;
+    const int craw = io.claim;
+    const int araw = io.arrival;
+    const int nbt_lo = io.bt_lo;
+    const int nbt_hi = io.bt_hi;
+
+    if (claiming) zi = 2 * W + C * __builtin_amdgcn_readfirstlane(craw) + wave % C;
+    // Z's descriptor is needed now only when this is X's last page and Y is
+    // a single page (Z's first page is then the next DMA); otherwise it is
+    // fetched after the compute below.
+    const bool z_now = claiming && zi < N && i + 1 == np && Y[2] - Y[1] == 1;
+    if (z_now) {
+      Z = desc_at(zi);
+      z_len = sload(p.seq_lens, Z[0]);
+    }
+    const bool merging = arriving && __builtin_amdgcn_readfirstlane(araw) == d_n - 1;
+
+    // The page after the one just issued (for X's last page: Y's second,
+    // or Z's first when Y is a single page).
+    if (i + 2 < np) {
+      fpg = page_of(bt_lo, bt_hi, i + 2);
+    } else if (i + 2 == np) {
+      fvalid = yi < N;
+      fh = Y[7];
+      fpg = page_of(nbt_lo, nbt_hi, 0);
+    } else if (yi < N) {
+      if (Y[2] - Y[1] > 1) {
+        fh = Y[7];
+        fpg = page_of(nbt_lo, nbt_hi, 1);
+      } else {
+        fvalid = zi < N;
+        if (fvalid) {
+          fh = Z[7];
+          fpg = sload(p.block_tables, (int64_t)Z[0] * p.bt_stride + Z[1]);
+          fpg = (fpg >= 0 && fpg < p.num_pages) ? fpg : 0;
+        }
+      }
+    }
+
+    const int pg = X[1] + i;
+    if ((pg + 1) * kPageSize > seq_len) compute(pg, cur, std::true_type{});
+    else compute(pg, cur, std::false_type{});
+    wave_lds_fence();
+    // Z's descriptor and length, fetched after this page's LDS reads so the
+    // scalar loads overlap the next page's wait.
+    __builtin_amdgcn_sched_barrier(0);
+    if (claiming && zi < N && !z_now) {
+      Z = desc_at(zi);
+      z_len = sload(p.seq_lens, Z[0]);
+    }
+    if (merging) {
+      const i32x8 D = desc_at(d_idx);
+      merge_partials<T>(p, D[0], D[7], D[5], D[4], D[6], lane, cur);
+    }
+    buf ^= 1;
+    if (++i < np) continue;
+
+    // ---- piece boundary ----
+    finish_piece();
+    if (X[4] > 1) {
+      b_ctr = X[0] * Hkv + X[7];
+      b_idx = xi;
+      b_n = X[4];
+    }
+    if (yi >= N) break;
+    xi = yi;
+    X = Y;
+    seq_len = y_len;
+    bt_lo = io.bt_lo;
+    bt_hi = io.bt_hi;
+    yi = zi;
+    Y = Z;
+    y_len = z_len;
+    zi = N;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qf[j] = io.qv[j];
+    np = X[2] - X[1];
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m = -INFINITY;
+    l = 0.f;
+    i = 0;
+  }
+
+  // Settle the split pieces whose arrivals are still pending (their stores
+  // are complete after the drain), then count this wavefront out; the last
+  // one resets the scheduler for the next launch.  Every claim this
+  // wavefront made has returned by now, so all claims precede the reset.
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);
+#pragma nounroll
+  for (int k = 0; k < 2; ++k) {
+    const int idx = k == 0 ? a_idx : b_idx;
+    const int ctr = k == 0 ? a_ctr : b_ctr;
+    if (idx >= 0) {
+      const i32x8 D = desc_at(idx);
+      int prev = 0;
+      if (lane == 0) prev = __hip_atomic_fetch_add(p.counters + ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__builtin_amdgcn_readfirstlane(prev) == D[4] - 1)
+        merge_partials<T>(p, D[0], D[7], D[5], D[4], D[6], lane, lds);
+    }
+  }
+  if (lane == 0) {
+    int* const exit_ctr = p.sched + kDecodeClaimCounters * kDecodeSchedLineInts;
+    const int gone = __hip_atomic_fetch_add(exit_ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (gone == W - 1) {
+      for (int k = 0; k < C; ++k)
+        __hip_atomic_store(p.sched + k * kDecodeSchedLineInts, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(exit_ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// Device-scope (coherent) load of a split-K log-sum-exp written by another CU.
+__device__ inline float ld_coherent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Cache-policy bits of a device-scope (sc1) global_load_lds.
+constexpr int kLoadLdsDeviceScope = 16;
+
+// Merges the n_chunks split-K partials of (sequence s, KV head h) into the
+// output rows of its G query heads:
+//   o = sum_k w_k o_k / sum_k w_k,  w_k = 2^(lse_k - max_k lse_k).
+// Lane L owns chunks L, L+64, ... in the log-sum-exp passes and output
+// columns d = 2L, 2L+1 in the weighted sum.  The partial rows of up to 16
+// (chunk, head) pairs at a time are copied into `scratch` (8 KB of the
+// wavefront's LDS) with coherent global_load_lds and summed from there, so a
+// merge costs a few memory round trips whatever G is, without holding the
+// rows in registers.  Resets the arrival counter for the next launch.
+template <typename T>
+__device__ inline void merge_partials(const DecodeParams& p, int s, int h, int pbase, int nchunks,
+                                      int64_t qrow, int lane, lds_u8* scratch) {
+  const int G = p.group;
   const int Hkv = p.num_kv_heads;
-  if (nchunks == 1) {
-    if (c < G) {
-      T* op = (T*)p.out + qrow * p.out_tok_stride + (int64_t)(h * G + c) * p.out_head_stride + 4 * q4;
+  const float* lse_base = p.part_lse + ((int64_t)pbase * Hkv + h) * G;  // chunk k: + k*Hkv*G
+  const int64_t lse_chunk = (int64_t)Hkv * G;
+  float mx[16];
 #pragma unroll
-      for (int mt = 0; mt < 8; ++mt) {
-        typename Elem<T>::v4 w;
+  for (int g = 0; g < 16; ++g) mx[g] = -INFINITY;
+  for (int k0 = 0; k0 < nchunks; k0 += 64) {
+    // Clamped chunk index: a repeated chunk leaves the maximum unchanged.
+    const float* row = lse_base + min(k0 + lane, nchunks - 1) * lse_chunk;
+    float v[16];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) w[r] = (T)(o[mt][r] * inv);
-        *reinterpret_cast<typename Elem<T>::v4*>(op + 16 * mt) = w;
-      }
+    for (int g = 0; g < 16; ++g)
+      if (g < G) v[g] = ld_coherent(row + g);
+#pragma unroll
+    for (int g = 0; g < 16; ++g)
+      if (g < G) mx[g] = fmaxf(mx[g], v[g]);
+  }
+#pragma unroll
+  for (int g = 0; g < 16; ++g) {
+    if (g < G) {
+      float v = mx[g];
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+      mx[g] = v;
     }
-    return;
   }
-
-  // Split-K: publish this chunk's normalised partial and log2-sum-exp with
-  // device-scope stores (written through past this XCD's L2), drain them,
-  // then count the chunk in.  This avoids a full L2 write-back/invalidate
-  // (what a device-scope fence costs on a multi-XCD part) per chunk.
-  const int64_t slot = (int64_t)(pbase + chunk) * Hkv + h;
-  if (c < G) {
-    float* po = p.part_o + (slot * G + c) * kHeadDim + 4 * q4;
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        __hip_atomic_store(po + 16 * mt + r, o[mt][r] * inv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (q4 == 0)
-      __hip_atomic_store(&p.part_lse[slot * G + c], l_tot > 0.f ? m + fast_log2(l_tot) : -INFINITY,
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  int prev = 0;
-  if (lane == 0)
-    prev = __hip_atomic_fetch_add(&p.counters[(int64_t)s * Hkv + h], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  prev = __shfl(prev, 0);
-  if (prev != nchunks - 1) return;
-
-  // Last chunk to arrive: merge all partials of this (sequence, KV head);
-  // device-scope loads read them from past the (per-XCD) L2.
+  // A chunk's G rows are contiguous (G * 512 bytes); `batch` chunks fill at
+  // most 16 rows of scratch.
+  const int batch = max(1, 16 / G);
+  const int64_t o_chunk = (int64_t)Hkv * G * kHeadDim;
+  const float* o_base = p.part_o + ((int64_t)pbase * Hkv + h) * G * kHeadDim;
+  const int pairs = (G + 1) / 2;  // 1 KB copies per chunk (two rows each)
   const int d = 2 * lane;
-  for (int g = 0; g < G; ++g) {
-    float mx = -INFINITY;
-    for (int k = 0; k < nchunks; ++k) {
-      const float lse = __hip_atomic_load(&p.part_lse[((int64_t)(pbase + k) * Hkv + h) * G + g],
-                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      mx = fmaxf(mx, lse);
-    }
-    float a0 = 0.f, a1 = 0.f, wsum = 0.f;
-    if (mx != -INFINITY) {
-      for (int k = 0; k < nchunks; ++k) {
-        const int64_t sl = ((int64_t)(pbase + k) * Hkv + h) * G + g;
-        const float lse = __hip_atomic_load(&p.part_lse[sl], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const float w = fast_exp2(lse - mx);
-        const float* po = p.part_o + sl * kHeadDim + d;
-        a0 += w * __hip_atomic_load(po, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        a1 += w * __hip_atomic_load(po + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        wsum += w;
+  float a0[16], a1[16], wsum[16];
+#pragma unroll
+  for (int g = 0; g < 16; ++g) a0[g] = a1[g] = wsum[g] = 0.f;
+  for (int k0 = 0; k0 < nchunks; k0 += 64) {
+    const int k = k0 + lane;
+    const float* row = lse_base + min(k, nchunks - 1) * lse_chunk;
+    float w[16];
+#pragma unroll
+    for (int g = 0; g < 16; ++g)
+      if (g < G) w[g] = ld_coherent(row + g);
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      if (g < G) {
+        w[g] = (k < nchunks && mx[g] != -INFINITY) ? fast_exp2(w[g] - mx[g]) : 0.f;
+        wsum[g] += w[g];
       }
     }
-    const float winv = wsum > 0.f ? 1.0f / wsum : 0.f;
-    T* op = (T*)p.out + qrow * p.out_tok_stride + (int64_t)(h * G + g) * p.out_head_stride + d;
-    op[0] = (T)(a0 * winv);
-    op[1] = (T)(a1 * winv);
+    const int cnt = min(64, nchunks - k0);
+    for (int j0 = 0; j0 < cnt; j0 += batch) {
+      const int nb = min(batch, cnt - j0);
+      // Row pair (2q, 2q+1) of chunk j0 + b lands at scratch + (b*G + 2q)*512;
+      // lanes 32..63 of an odd G's last pair re-read row 2q (in bounds) into
+      // the next row slot, which nothing reads.
+      for (int b = 0; b < nb; ++b) {
+        const float* src = o_base + (int64_t)(k0 + j0 + b) * o_chunk;
+        for (int q = 0; q < pairs; ++q) {
+          const int r = min(2 * q + (lane >> 5), G - 1);
+          dma16_policy<kLoadLdsDeviceScope>(src + r * kHeadDim + 4 * (lane & 31),
+                                            scratch + (b * G + 2 * q) * 512);
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);
+      wave_lds_fence();
+      for (int b = 0; b < nb; ++b) {
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+          if (g < G) {
+            const float wb = __builtin_bit_cast(
+                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w[g]), j0 + b));
+            const f32x2 v = lds_ld8<f32x2>(scratch + (b * G + g) * 512 + 4 * d);
+            a0[g] += wb * v.x;
+            a1[g] += wb * v.y;
+          }
+        }
+      }
+      wave_lds_fence();
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < 16; ++g) {
+    if (g < G) {
+      float ws = wsum[g];
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) ws += __shfl_xor(ws, off);
+      const float winv = ws > 0.f ? 1.0f / ws : 0.f;
+      T* op = (T*)p.out + qrow * p.out_tok_stride + (int64_t)(h * G + g) * p.out_head_stride + d;
+      op[0] = (T)(a0[g] * winv);
+      op[1] = (T)(a1[g] * winv);
+    }
   }
   if (lane == 0)
     __hip_atomic_store(&p.counters[(int64_t)s * Hkv + h], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // Leave no store outstanding: the decode loop's waits assume none is.
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);
 }
 
 }  // namespace mva

@@ -8,29 +8,25 @@ namespace {
 
 template <typename T>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_kernel(DecodeParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t vbuf0[kDecodeVBufBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t vbuf1[kDecodeVBufBytes];
-  // KV head varies fastest so the head slices of one page are requested
-  // close together in time (the page's K/V are contiguous 32 KB runs).
-  const int h = (int)(blockIdx.x % (uint32_t)p.num_kv_heads);
-  const int item = (int)(blockIdx.x / (uint32_t)p.num_kv_heads);
-  decode_item<T>(p, p.items + (int64_t)item * kDecodeItemInts, h, (lds_u8*)vbuf0, (lds_u8*)vbuf1);
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kDecodeWaveLdsBytes];
+  decode_wave<T>(p, (int)blockIdx.x, (lds_u8*)lds);
 }
 
 }  // namespace
 
 static int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
-// Workspace layout: [counters int32 num_seqs*Hkv][lse f32 slots*Hkv*G][o f32 slots*Hkv*G*D].
+// Workspace layout: [scheduler (kDecodeSchedBytes)][counters int32 num_seqs*Hkv]
+// [lse f32 slots*Hkv*G][o f32 slots*Hkv*G*D].
 int64_t decode_workspace_bytes(int64_t num_seqs, int64_t slots, int hkv, int group) {
-  return align256(num_seqs * hkv * 4) + align256(slots * hkv * group * 4) +
+  return kDecodeSchedBytes + align256(num_seqs * hkv * 4) + align256(slots * hkv * group * 4) +
          align256(slots * hkv * group * kHeadDim * 4);
 }
 
 int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, int64_t q_head_stride,
                        const void* k_cache, const void* v_cache, int64_t num_pages, int64_t page_stride,
                        int64_t token_stride, const int32_t* block_tables, int64_t block_table_stride,
-                       const int32_t* seq_lens, const int32_t* items, int64_t num_items,
+                       const int32_t* seq_lens, const int32_t* items, int64_t num_items, int64_t num_waves,
                        int64_t num_seqs, int64_t num_part_slots, void* out, int64_t out_token_stride,
                        int64_t out_head_stride, void* workspace, int64_t workspace_bytes,
                        int num_q_heads, int num_kv_heads, int head_dim, int page_size,
@@ -42,6 +38,9 @@ int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, i
   const int group = num_q_heads / num_kv_heads;
   if (group > 16) return set_error("paged attention: at most 16 query heads per KV head");
   if (num_items < 0 || num_items > 0x7fffffffLL) return set_error("paged attention: invalid item count");
+  if (num_waves < 0 || num_waves > 0x7fffffffLL) return set_error("paged attention: invalid wave count");
+  if (num_items > 0 && (num_waves <= 0 || num_waves > num_items))
+    return set_error("paged attention: num_waves must be in [1, num_items]");
   if (num_pages <= 0) return set_error("paged attention: empty KV cache");
   const uint64_t align_bits = (uint64_t)(uintptr_t)q | (uint64_t)(uintptr_t)k_cache |
                               (uint64_t)(uintptr_t)v_cache | (uint64_t)(q_token_stride * 2) |
@@ -52,7 +51,7 @@ int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, i
     return set_error("paged attention: output buffer and strides must be 8-byte aligned");
   if (workspace_bytes < decode_workspace_bytes(num_seqs, num_part_slots, num_kv_heads, group))
     return set_error("paged attention: workspace too small");
-  if (num_part_slots > 0 && workspace == nullptr) return set_error("paged attention: missing workspace");
+  if (num_items > 0 && workspace == nullptr) return set_error("paged attention: missing workspace");
   p.q = q;
   p.q_tok_stride = q_token_stride;
   p.q_head_stride = q_head_stride;
@@ -66,10 +65,13 @@ int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, i
   p.seq_lens = seq_lens;
   p.items = items;
   p.num_items = (int)num_items;
+  p.num_waves = (int)num_waves;
   p.out = out;
   p.out_tok_stride = out_token_stride;
   p.out_head_stride = out_head_stride;
   uint8_t* ws = (uint8_t*)workspace;
+  p.sched = (int32_t*)ws;
+  ws += kDecodeSchedBytes;
   p.counters = (int32_t*)ws;
   ws += align256(num_seqs * num_kv_heads * 4);
   p.part_lse = (float*)ws;
@@ -92,7 +94,8 @@ extern "C" int mva_paged_decode(const void* q, int64_t q_token_stride, int64_t q
                                 const void* k_cache, const void* v_cache, int64_t num_pages,
                                 int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
                                 int64_t block_table_stride, const int32_t* seq_lens,
-                                const int32_t* items, int64_t num_items, int64_t num_seqs,
+                                const int32_t* items, int64_t num_items, int64_t num_waves,
+                                int64_t num_seqs,
                                 int64_t num_part_slots, void* out, int64_t out_token_stride,
                                 int64_t out_head_stride, void* workspace, int64_t workspace_bytes,
                                 int num_q_heads, int num_kv_heads, int head_dim, int page_size,
@@ -101,13 +104,13 @@ extern "C" int mva_paged_decode(const void* q, int64_t q_token_stride, int64_t q
   DecodeParams p;
   int rc = fill_decode_params(p, q, q_token_stride, q_head_stride, k_cache, v_cache, num_pages,
                               page_stride, token_stride, block_tables, block_table_stride, seq_lens,
-                              items, num_items, num_seqs, num_part_slots, out, out_token_stride,
+                              items, num_items, num_waves, num_seqs, num_part_slots, out,
+                              out_token_stride,
                               out_head_stride, workspace, workspace_bytes, num_q_heads, num_kv_heads,
                               head_dim, page_size, softmax_scale);
   if (rc) return rc;
   if (num_items == 0) return 0;
-  if (num_items * num_kv_heads > 0x7fffffffLL) return set_error("paged attention: too many work items");
-  const dim3 grid((uint32_t)(num_items * num_kv_heads));
+  const dim3 grid((uint32_t)num_waves);
   hipStream_t s = (hipStream_t)stream;
   if (dtype == kBF16) hipLaunchKernelGGL(paged_decode_kernel<__bf16>, grid, dim3(64), 0, s, p);
   else if (dtype == kF16) hipLaunchKernelGGL(paged_decode_kernel<_Float16>, grid, dim3(64), 0, s, p);

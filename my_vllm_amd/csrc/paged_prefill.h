@@ -224,12 +224,12 @@ __device__ void prefill_item(const PrefillParams& p, const int32_t* __restrict__
     const lds_u8* vlane = vb + (4 * hi + (ti >> 2)) * 64 + (2 * dgrp + ((ti >> 1) & 1)) * 16 + (ti & 1) * 8;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
+      // Reads for (dt, j) sit at byte dt*1024 + j*512 past block 4*kk.
+      s16x4 vt[8];
+      lds_ld_tr16_x8_stride512(vlane + 4 * kk * 1024, vt);
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const lds_u8* a0 = vlane + (4 * kk + dt) * 1024;
-        const s16x4 va = lds_ld_tr16(a0);
-        const s16x4 vbv = lds_ld_tr16(a0 + 8 * 64);
-        const s16x8 both = __builtin_shufflevector(va, vbv, 0, 1, 2, 3, 4, 5, 6, 7);
+        const s16x8 both = __builtin_shufflevector(vt[2 * dt], vt[2 * dt + 1], 0, 1, 2, 3, 4, 5, 6, 7);
         o[dt] = Elem<T>::mfma32(__builtin_bit_cast(V8, both), pf[kk], o[dt]);
       }
       __builtin_amdgcn_sched_barrier(0);

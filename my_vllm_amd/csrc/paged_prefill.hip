@@ -9,7 +9,7 @@ int64_t decode_workspace_bytes(int64_t num_seqs, int64_t slots, int hkv, int gro
 int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, int64_t q_head_stride,
                        const void* k_cache, const void* v_cache, int64_t num_pages, int64_t page_stride,
                        int64_t token_stride, const int32_t* block_tables, int64_t block_table_stride,
-                       const int32_t* seq_lens, const int32_t* items, int64_t num_items,
+                       const int32_t* seq_lens, const int32_t* items, int64_t num_items, int64_t num_waves,
                        int64_t num_seqs, int64_t num_part_slots, void* out, int64_t out_token_stride,
                        int64_t out_head_stride, void* workspace, int64_t workspace_bytes,
                        int num_q_heads, int num_kv_heads, int head_dim, int page_size,
@@ -39,15 +39,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     return;
   }
   const int w = threadIdx.x >> 6;
-  const int64_t pair = (int64_t)(blockIdx.x - n_prefill_wgs) * 4 + w;
-  if (pair >= (int64_t)dp.num_items * dp.num_kv_heads) return;
-  const int h = (int)(pair % dp.num_kv_heads);
-  const int64_t item = pair / dp.num_kv_heads;
-  lds_u8* mine = (lds_u8*)lds + w * 2 * kDecodeVBufBytes;
-  decode_item<T>(dp, dp.items + item * kDecodeItemInts, h, mine, mine + kDecodeVBufBytes);
+  const int64_t wave = (int64_t)(blockIdx.x - n_prefill_wgs) * 4 + w;
+  if (wave >= dp.num_waves) return;
+  decode_wave<T>(dp, (int)wave, (lds_u8*)lds + w * kDecodeWaveLdsBytes);
 }
 
-static_assert(4 * 2 * kDecodeVBufBytes <= kPrefillLdsBytes, "decode buffers must fit the prefill LDS");
+static_assert(4 * kDecodeWaveLdsBytes <= kPrefillLdsBytes, "decode buffers must fit the prefill LDS");
 
 }  // namespace
 
@@ -133,7 +130,8 @@ extern "C" int mva_paged_mixed(const void* q, int64_t q_token_stride, int64_t q_
                                int64_t block_table_stride, const int32_t* seq_lens,
                                const int32_t* query_start_loc, const int32_t* prefill_items,
                                int64_t num_prefill_items, const int32_t* decode_items,
-                               int64_t num_decode_items, int64_t num_seqs, int64_t num_part_slots,
+                               int64_t num_decode_items, int64_t num_decode_waves, int64_t num_seqs,
+                               int64_t num_part_slots,
                                void* out, int64_t out_token_stride, int64_t out_head_stride,
                                void* workspace, int64_t workspace_bytes, int num_q_heads,
                                int num_kv_heads, int head_dim, int page_size, float softmax_scale,
@@ -148,12 +146,13 @@ extern "C" int mva_paged_mixed(const void* q, int64_t q_token_stride, int64_t q_
   DecodeParams dp;
   rc = fill_decode_params(dp, q, q_token_stride, q_head_stride, k_cache, v_cache, num_pages, page_stride,
                           token_stride, block_tables, block_table_stride, seq_lens, decode_items,
-                          num_decode_items, num_seqs, num_part_slots, out, out_token_stride, out_head_stride,
+                          num_decode_items, num_decode_waves, num_seqs, num_part_slots, out,
+                          out_token_stride, out_head_stride,
                           workspace, workspace_bytes, num_q_heads, num_kv_heads, head_dim, page_size,
                           softmax_scale);
   if (rc) return rc;
   const int64_t n_prefill_wgs = num_prefill_items * num_kv_heads;
-  const int64_t n_decode_wgs = (num_decode_items * num_kv_heads + 3) / 4;
+  const int64_t n_decode_wgs = num_decode_items > 0 ? (num_decode_waves + 3) / 4 : 0;
   if (n_prefill_wgs + n_decode_wgs > 0x7fffffffLL) return set_error("paged attention: too many work items");
   if (n_prefill_wgs + n_decode_wgs == 0) return 0;
   const dim3 grid((uint32_t)(n_prefill_wgs + n_decode_wgs));

@@ -15,7 +15,7 @@ HEAD_DIM = 128
 PAGE_SIZE = 16
 # int32 fields per decode work item (kDecodeItemInts in csrc/paged_decode.h).
 DECODE_ITEM_INTS = 8
-# Longest chunk one decode work item may cover (kMaxChunkPages).
+# Longest piece one decode work item may cover (kMaxChunkPages).
 MAX_CHUNK_PAGES = 128
 # Query rows per prefill workgroup (kPrefillRows): G heads x 128 // G tokens.
 PREFILL_ROWS = 128
@@ -135,16 +135,18 @@ def paged_decode(
     seq_lens: torch.Tensor,
     items: torch.Tensor,
     num_items: int,
+    num_waves: int,
     num_seqs: int,
     num_part_slots: int,
     out: torch.Tensor,
     workspace: torch.Tensor | None,
     softmax_scale: float,
 ) -> None:
-    """Launch the paged GQA decode kernel over prepared work items.
+    """Launch the paged GQA decode kernel over prepared pieces.
 
-    ``q``/``out`` are ``[T, Hq, D]`` views (rows addressed by the items'
-    ``q_row``); caches ``[P, page, Hkv, D]``; ``items`` int32 ``[n, 8]``.
+    ``q``/``out`` are ``[T, Hq, D]`` views (rows addressed by the pieces'
+    ``q_row``); caches ``[P, page, Hkv, D]``; ``items`` int32 ``[n, 8]``,
+    claimed by ``num_waves`` (``1 <= num_waves <= n``) wavefronts.
     """
     num_q_heads, head_dim = q.shape[1], q.shape[2]
     num_pages, page_size, num_kv_heads = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
@@ -155,7 +157,7 @@ def paged_decode(
         q.data_ptr(), q.stride(0), q.stride(1),
         k_cache.data_ptr(), v_cache.data_ptr(), num_pages, k_cache.stride(0), k_cache.stride(1),
         block_tables.data_ptr(), block_tables.stride(0), seq_lens.data_ptr(),
-        items.data_ptr(), num_items, num_seqs, num_part_slots,
+        items.data_ptr(), num_items, num_waves, num_seqs, num_part_slots,
         out.data_ptr(), out.stride(0), out.stride(1),
         ws_ptr, ws_bytes,
         num_q_heads, num_kv_heads, head_dim, page_size, float(softmax_scale),
@@ -214,15 +216,16 @@ def paged_mixed(
     query_start_loc: torch.Tensor,
     prefill_items: torch.Tensor,
     num_prefill_items: int,
-    decode_items: torch.Tensor,
+    decode_items: torch.Tensor | None,
     num_decode_items: int,
+    num_decode_waves: int,
     num_seqs: int,
     num_part_slots: int,
     out: torch.Tensor,
     workspace: torch.Tensor | None,
     softmax_scale: float,
 ) -> None:
-    """One launch: prefill tiles write ``out[:P]``, decode items write ``out[P:]``."""
+    """One launch: prefill tiles write ``out[:P]``, decode pieces write ``out[P:]``."""
     ws_ptr = workspace.data_ptr() if workspace is not None else 0
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _native.call(
@@ -230,7 +233,8 @@ def paged_mixed(
         *_paged_args(q, k_cache, v_cache, block_tables, seq_lens),
         query_start_loc.data_ptr(),
         prefill_items.data_ptr(), num_prefill_items,
-        decode_items.data_ptr(), num_decode_items, num_seqs, num_part_slots,
+        decode_items.data_ptr() if decode_items is not None else 0, num_decode_items, num_decode_waves,
+        num_seqs, num_part_slots,
         out.data_ptr(), out.stride(0), out.stride(1),
         ws_ptr, ws_bytes,
         *_tail_args(q, k_cache, softmax_scale),

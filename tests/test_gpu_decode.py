@@ -10,7 +10,16 @@ cache rows, fp16, and repeated launches over one workspace.
 import pytest
 import torch
 
-from my_vllm_amd.attention_backend import AttentionBackendRegistry, AttentionRoute, MI355XAttentionBackend
+import numpy as np
+
+from my_vllm_amd import ops
+from my_vllm_amd.attention_backend import (
+    AttentionBackendRegistry,
+    AttentionRoute,
+    MI355XAttentionBackend,
+    _to_device,
+    make_decode_plan,
+)
 from my_vllm_amd.context import BatchType
 from my_vllm_amd.workloads import config_decode_small, decode_lengths, make_paged_batch
 from oracle.reference import paged_attention
@@ -66,13 +75,16 @@ def test_gqa_ratios(gpu, hq, hkv):
     assert_attention_close(out, _expected(batch))
 
 
-@pytest.mark.parametrize("chunk_pages", [8, 10, 128])
-def test_split_k_merge(gpu, monkeypatch, chunk_pages):
-    monkeypatch.setenv("MVA_DECODE_CHUNK_PAGES", str(chunk_pages))
+@pytest.mark.parametrize("waves", [1, 7, 64, 2048, 100000])
+def test_split_k_merge(gpu, monkeypatch, waves):
+    # The piece length follows the wave count: 1 wave claims every piece
+    # (128-page pieces) itself; 100000 waves give 4-page pieces and one
+    # wavefront per piece.
+    monkeypatch.setenv("MVA_DECODE_WAVES", str(waves))
     ctx = [1, 16, 17, 255, 256, 257, 1000, 3001, 4096, 2049]
     batch = make_paged_batch(43, [1] * len(ctx), ctx, 0, 32, 8)
     out, backend, plan, args = _run(batch, gpu)
-    assert plan.metadata.decode_chunk_pages == chunk_pages
+    assert plan.metadata.num_decode_part_slots > 0
     expected = _expected(batch)
     assert_attention_close(out, expected)
     first = out.clone()
@@ -82,8 +94,33 @@ def test_split_k_merge(gpu, monkeypatch, chunk_pages):
     assert torch.equal(again, first)
 
 
+@pytest.mark.parametrize("waves,per_wave,min_pages", [(1, 1, 1), (3, 8, 1), (64, 2, 1), (5000, 64, 1), (40, 4, 2)])
+def test_piece_plans_through_c_abi(gpu, waves, per_wave, min_pages):
+    # One-page pieces, one-page sequences and single-piece wavefronts exercise
+    # every branch of the page stream across piece boundaries; a second launch
+    # checks that the scheduler and arrival counters were reset.
+    ctx = [1, 16, 17, 40, 1, 300, 33, 2049, 5, 640]
+    hq, hkv = 32, 8
+    batch = make_paged_batch(61, [1] * len(ctx), ctx, 0, hq, hkv)
+    common, q, kc, vc = _to(batch, gpu)
+    counts = np.asarray([(n + 15) // 16 for n in ctx])
+    items, nw, slots = make_decode_plan(counts, 0, 0, hkv, waves, per_wave, min_pages)
+    assert nw == min(waves, items.shape[0])
+    ws = torch.zeros(ops.decode_workspace_bytes(len(ctx), slots, hkv, hq // hkv), dtype=torch.uint8, device=gpu)
+    out = torch.full_like(q, float("nan"))
+    scale = 128 ** -0.5
+    args = (q, kc, vc, common.block_tables, common.seq_lens, _to_device(items, gpu), items.shape[0], nw,
+            len(ctx), slots, out, ws, scale)
+    ops.paged_decode(*args)
+    first = out.clone()
+    assert_attention_close(first, _expected(batch))
+    ops.paged_decode(*args)
+    assert torch.equal(out, first)
+    assert int(ws[:8].view(torch.int32).abs().sum().item()) == 0
+
+
 def test_stale_nan_rows_past_seq_len_do_not_leak(gpu, monkeypatch):
-    monkeypatch.setenv("MVA_DECODE_CHUNK_PAGES", "8")
+    monkeypatch.setenv("MVA_DECODE_WAVES", "100000")
     ctx = [5, 16, 33, 300, 129]
     batch = make_paged_batch(47, [1] * len(ctx), ctx, 0, 16, 8, extra_pages=3)
     bt = batch.common.block_tables

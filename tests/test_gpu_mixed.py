@@ -18,9 +18,9 @@ from tests.test_gpu_prefill import expected, run_backend
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("chunk", ["8", "128"])
-def test_mixed_unified_and_split_match(gpu, monkeypatch, chunk):
-    monkeypatch.setenv("MVA_DECODE_CHUNK_PAGES", chunk)
+@pytest.mark.parametrize("waves", ["3", "2048", "100000"])
+def test_mixed_unified_and_split_match(gpu, monkeypatch, waves):
+    monkeypatch.setenv("MVA_DECODE_WAVES", waves)
     q = [5, 130, 1, 1, 1, 1]
     kv = [21, 400, 13, 18, 1500, 3000]
     batch = make_paged_batch(83, q, kv, 2, 32, 8)
