@@ -425,6 +425,9 @@ class MI355XAttentionBackendMixin:
     route_type: type = AttentionRoute
     batch_type_enum: type = BatchType
     common_type: type = CommonAttentionMetadata
+    # Metadata tensors must live on the GPU (the reference's contract,
+    # attention_backend.py:1436-1440); host-only planning tests relax it.
+    require_device_metadata = True
 
     def __init__(
         self,
@@ -508,7 +511,7 @@ class MI355XAttentionBackendMixin:
 
     # ---- per-step metadata and plan ------------------------------------------
     def build_metadata(self, common) -> MI355XAttentionMetadata:
-        _validate_common_metadata(common, require_cuda=True, common_type=self.common_type)
+        _validate_common_metadata(common, require_cuda=self.require_device_metadata, common_type=self.common_type)
         if common.block_tables is None:
             return MI355XAttentionMetadata(
                 query_start_loc=common.query_start_loc,

@@ -196,3 +196,27 @@ def slot_mapping_for(
         block_table[pos // block_size] * block_size + pos % block_size
         for pos in range(num_cached_tokens, num_context_tokens)
     ]
+
+
+def split_page_csr(query_start_loc: list[int], kv_indptr: list[int], page_indices: list[int],
+                   last_page_len: list[int], num_prefill_seqs: int, num_prefill_pages: int):
+    """MIXED_SPLIT slicing of the page CSR into a prefill part and a decode part.
+
+    Restates nanovllm/layers/attention_backend.py:858-889: the prefill plan
+    takes the first ``num_prefill_seqs + 1`` offsets and the first
+    ``num_prefill_pages`` pages; the decode plan takes the rest, with its
+    ``kv_indptr`` re-based by ``num_prefill_pages`` (:874-876).
+    """
+    p = num_prefill_seqs
+    prefill = {
+        "qo_indptr": list(query_start_loc[: p + 1]),
+        "kv_indptr": list(kv_indptr[: p + 1]),
+        "page_indices": list(page_indices[:num_prefill_pages]),
+        "last_page_len": list(last_page_len[:p]),
+    }
+    decode = {
+        "kv_indptr": [x - num_prefill_pages for x in kv_indptr[p:]],
+        "page_indices": list(page_indices[num_prefill_pages:]),
+        "last_page_len": list(last_page_len[p:]),
+    }
+    return prefill, decode

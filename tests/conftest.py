@@ -13,6 +13,16 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and the built native library")
 
 
+def pytest_sessionstart(session):
+    """Build the C-ABI library when a checkout has none yet (it is not committed)."""
+    from my_vllm_amd import _native
+
+    if not _native.LIB_PATH.exists():
+        from my_vllm_amd import build
+
+        build.build()
+
+
 @pytest.fixture(scope="session")
 def gpu():
     """The GPU device; fails (does not skip) when the GPU or the native library is missing."""

@@ -1,0 +1,258 @@
+"""CPU: host-side logic of the MI355X backend (no kernel launches).
+
+Covers the reference contract the backend mirrors (registry, validation,
+classification, plan routes, trusted planning without device reads) and the
+work-list planners the kernels consume.  Metadata tensors stay on the CPU
+through the ``require_device_metadata`` seam; nothing here calls a kernel.
+"""
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from my_vllm_amd import ops
+from my_vllm_amd.attention_backend import (
+    AttentionBackend,
+    AttentionBackendRegistry,
+    AttentionPlan,
+    AttentionRoute,
+    MI355XAttentionBackend,
+    MI355XAttentionMetadata,
+    MI355XSplitAttentionBackend,
+    make_decode_plan,
+    make_prefill_items,
+)
+from my_vllm_amd.context import BatchType, CommonAttentionMetadata
+
+KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
+
+
+class HostBackend(MI355XAttentionBackend):
+    require_device_metadata = False
+
+
+class HostSplitBackend(MI355XSplitAttentionBackend):
+    require_device_metadata = False
+
+
+def _common(q_lens, kv_lens, num_prefill, *, trusted=False, cache=True):
+    qsl = [0]
+    for n in q_lens:
+        qsl.append(qsl[-1] + n)
+    counts = tuple((n + 15) // 16 for n in kv_lens)
+    bt = None
+    if cache:
+        width, rows, page = max(counts), [], 0
+        for c in counts:
+            rows.append(list(range(page, page + c)) + [-1] * (width - c))
+            page += c
+        bt = torch.tensor(rows, dtype=torch.int32)
+    return CommonAttentionMetadata(
+        num_prefill_seqs=num_prefill,
+        num_decode_seqs=len(q_lens) - num_prefill,
+        num_prefill_tokens=sum(q_lens[:num_prefill]),
+        num_decode_tokens=sum(q_lens[num_prefill:]),
+        query_start_loc=torch.tensor(qsl, dtype=torch.int32),
+        seq_lens=torch.tensor(kv_lens, dtype=torch.int32),
+        slot_mapping=torch.arange(qsl[-1], dtype=torch.int32),
+        block_tables=bt,
+        max_q_len=max(q_lens),
+        max_kv_len=max(kv_lens),
+        block_counts=counts if cache else (),
+        num_kv_blocks=sum(counts) if cache else 0,
+        num_prefill_kv_blocks=sum(counts[:num_prefill]) if cache else 0,
+        trusted=trusted,
+    )
+
+
+def test_page_csr_known_answer_through_backend_metadata():
+    kat = KATS["page_csr"]
+    backend = HostBackend(16, 4, 128, 16, torch.bfloat16)
+    md = backend.build_metadata(_common(kat["query_lengths"], kat["kv_lengths"], kat["num_prefill_seqs"]))
+    assert isinstance(md, MI355XAttentionMetadata)
+    assert list(md.kv_indptr) == kat["kv_indptr"]
+    assert md.num_pages == kat["num_pages"]
+    assert md.num_prefill_pages == kat["num_prefill_pages"]
+
+
+@pytest.mark.parametrize(
+    "q_lens,kv_lens,num_prefill,batch,route,split_route",
+    [
+        ((5, 3), (21, 13), 2, BatchType.PURE_PREFILL, AttentionRoute.PREFILL, AttentionRoute.PREFILL),
+        ((1, 1), (21, 13), 0, BatchType.PURE_DECODE, AttentionRoute.DECODE, AttentionRoute.DECODE),
+        ((5, 1), (21, 13), 1, BatchType.MIXED, AttentionRoute.MIXED_UNIFIED, AttentionRoute.MIXED_SPLIT),
+        ((1, 1), (1, 17), 1, BatchType.MIXED, AttentionRoute.MIXED_UNIFIED, AttentionRoute.MIXED_SPLIT),
+    ],
+)
+@pytest.mark.parametrize("trusted", [False, True])
+def test_plan_routes(q_lens, kv_lens, num_prefill, batch, route, split_route, trusted):
+    # Reference cases: tests/test_attention_backend.py:367-418 shapes and the
+    # all-single-token MIXED batch of tests/test_model_runner_metadata.py:351-374.
+    common = _common(q_lens, kv_lens, num_prefill, trusted=trusted)
+    plan = HostBackend(16, 4, 128, 16, torch.bfloat16).build_plan(common)
+    assert isinstance(plan, AttentionPlan)
+    assert plan.batch_type is batch and plan.route is route and plan.common is common
+    split = HostSplitBackend(16, 4, 128, 16, torch.bfloat16).build_plan(common)
+    assert split.batch_type is batch and split.route is split_route
+
+
+def test_cacheless_batch_plans_warmup():
+    plan = HostBackend(16, 4, 128, 16, torch.bfloat16).build_plan(_common((3, 1), (3, 1), 2, cache=False))
+    assert plan.route is AttentionRoute.WARMUP and plan.metadata.is_cacheless
+
+
+def test_trusted_planning_reads_no_device_values(monkeypatch):
+    # Trusted metadata is planned from host ints only (reference
+    # tests/test_attention_backend.py:529-553): no .item()/.cpu()/.tolist().
+    common = _common((5, 1, 1), (21, 13, 300), 1, trusted=True)
+    backend = HostBackend(16, 4, 128, 16, torch.bfloat16)
+
+    def forbidden(*args, **kwargs):
+        raise AssertionError("device read during trusted planning")
+
+    for name in ("item", "cpu", "tolist", "numpy"):
+        monkeypatch.setattr(torch.Tensor, name, forbidden)
+    plan = backend.build_plan(common)
+    monkeypatch.undo()
+    assert plan.route is AttentionRoute.MIXED_UNIFIED
+    assert plan.metadata.num_decode_items > 0 and plan.metadata.num_prefill_items > 0
+
+
+def test_validation_errors_follow_the_reference():
+    backend = HostBackend(16, 4, 128, 16, torch.bfloat16)
+    good = _common((5, 1), (21, 13), 1)
+    with pytest.raises(TypeError):
+        backend.build_plan(object())
+    bad_decode = _common((5, 2), (21, 13), 1)
+    with pytest.raises(ValueError, match="one query token"):
+        backend.build_plan(bad_decode)
+    wrong_dtype = CommonAttentionMetadata(**{**good.__dict__, "seq_lens": good.seq_lens.long()})
+    with pytest.raises(TypeError, match="int32"):
+        backend.build_plan(wrong_dtype)
+    device_backend = MI355XAttentionBackend(16, 4, 128, 16, torch.bfloat16)
+    with pytest.raises(ValueError, match="CUDA"):
+        device_backend.build_plan(good)
+
+
+def test_forward_rejects_foreign_plans_and_mismatched_caches():
+    backend = HostBackend(16, 4, 128, 16, torch.bfloat16)
+    plan = backend.build_plan(_common((1, 1), (21, 13), 0))
+    q = torch.zeros(2, 16, 128, dtype=torch.bfloat16)
+    cache = torch.zeros(4, 16, 4, 128, dtype=torch.bfloat16)
+    empty = q.new_empty((0, 4, 128))
+    with pytest.raises(TypeError):
+        backend.forward(q, empty, empty, cache, cache, object())
+    foreign = AttentionPlan(plan.batch_type, plan.route, plan.common, object())
+    with pytest.raises(TypeError):
+        backend.forward(q, empty, empty, cache, cache, foreign)
+    with pytest.raises(ValueError):
+        backend.forward(q, empty, empty, cache, empty, plan)
+
+
+def test_constructor_contract():
+    with pytest.raises(ValueError):
+        MI355XAttentionBackend(16, 4, 64, 16, torch.bfloat16)
+    with pytest.raises(ValueError):
+        MI355XAttentionBackend(16, 4, 128, 32, torch.bfloat16)
+    with pytest.raises(TypeError):
+        MI355XAttentionBackend(16, 4, 128, 16, torch.float32)
+    with pytest.raises(ValueError):
+        MI355XAttentionBackend(16, 5, 128, 16, torch.bfloat16)
+    backend = MI355XAttentionBackend(16, 4, 128, 16, torch.float16)
+    assert backend.softmax_scale == pytest.approx(128 ** -0.5)
+
+
+def test_support_reason_names_the_missing_capability():
+    reason = MI355XAttentionBackend.support_reason(
+        num_q_heads=16, num_kv_heads=4, head_dim=128, block_size=16, dtype=torch.bfloat16, device="cpu"
+    )
+    assert isinstance(reason, str) and reason
+    assert MI355XAttentionBackend.supports(num_q_heads=16, num_kv_heads=4, head_dim=64, block_size=16,
+                                           dtype=torch.bfloat16, device="cpu") is False
+
+
+def test_registry_contract():
+    names = AttentionBackendRegistry.names()
+    assert "mi355x" in names and "mi355x_split" in names
+    assert issubclass(AttentionBackendRegistry._BACKENDS["mi355x"], AttentionBackend)
+    with pytest.raises(ValueError):
+        AttentionBackendRegistry.register("auto", MI355XAttentionBackend)
+    with pytest.raises(ValueError):
+        AttentionBackendRegistry.register("", MI355XAttentionBackend)
+    with pytest.raises(ValueError):
+        AttentionBackendRegistry.register("mi355x", MI355XAttentionBackend)
+    with pytest.raises(TypeError):
+        AttentionBackendRegistry.register("not_a_backend", object)
+    with pytest.raises(RuntimeError):
+        # No gfx950 device in a CPU-only process: creation names the reason.
+        AttentionBackendRegistry.create("mi355x", num_q_heads=16, num_kv_heads=4, head_dim=128, block_size=16,
+                                        dtype=torch.bfloat16, device="cpu")
+
+
+# ---------------------------------------------------------------------------
+# Work-list planners
+# ---------------------------------------------------------------------------
+
+def _check_decode_plan(counts, hkv, waves, per_wave, min_pages):
+    items, nw, slots = make_decode_plan(np.asarray(counts), 3, 7, hkv, waves, per_wave, min_pages)
+    assert items.dtype == np.int32 and items.shape[1] == ops.DECODE_ITEM_INTS
+    assert 1 <= nw <= len(items) and nw <= waves
+    seen = {}
+    for s, pb, pe, ch, nc, base, qrow, h in items.tolist():
+        i = s - 3
+        assert qrow == 7 + i and 0 <= h < hkv and 0 <= pb < pe <= counts[i] and pe - pb <= ops.MAX_CHUNK_PAGES
+        seen.setdefault((i, h), []).append((pb, pe, ch, nc, base))
+    assert len(seen) == len(counts) * hkv
+    used = set()
+    for (i, h), pieces in seen.items():
+        pieces.sort()
+        nc = pieces[0][3]
+        assert len(pieces) == nc and {p[3] for p in pieces} == {nc}
+        assert pieces[0][0] == 0 and pieces[-1][1] == counts[i]
+        assert all(a[1] == b[0] for a, b in zip(pieces, pieces[1:]))
+        assert sorted(p[2] for p in pieces) == list(range(nc))
+        if nc > 1:
+            base = pieces[0][4]
+            assert all(p[4] == base for p in pieces)
+            assert not used & set(range(base, base + nc)) and base + nc <= slots
+            used |= set(range(base, base + nc))
+    lengths = items[:, 2] - items[:, 1]
+    assert np.all(np.diff(lengths) <= 0), "pieces are listed longest first"
+    return items, nw, slots
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_decode_plan_covers_every_page_once(seed):
+    rng = np.random.default_rng(seed)
+    counts = rng.integers(1, 400, size=int(rng.integers(1, 40))).tolist()
+    _check_decode_plan(counts, int(rng.choice([1, 2, 8])), int(rng.integers(1, 5000)),
+                       int(rng.integers(1, 9)), int(rng.integers(1, 9)))
+
+
+def test_decode_plan_edges():
+    items, nw, slots = _check_decode_plan([1], 1, 2048, 4, 4)
+    assert len(items) == 1 and nw == 1 and slots == 0
+    items, nw, _ = _check_decode_plan([300], 8, 1, 1, 4)
+    assert nw == 1 and (items[:, 2] - items[:, 1]).max() <= ops.MAX_CHUNK_PAGES
+    empty, nw, slots = make_decode_plan(np.zeros(0, np.int64), 0, 0, 8, 2048)
+    assert empty.shape == (0, ops.DECODE_ITEM_INTS) and nw == 0 and slots == 0
+    with pytest.raises(ValueError):
+        make_decode_plan(np.array([0]), 0, 0, 8, 2048)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_prefill_items_cover_every_tile_once(seed):
+    rng = np.random.default_rng(100 + seed)
+    q_ub = rng.integers(1, 700, size=int(rng.integers(1, 12)))
+    kv_ub = q_ub + rng.integers(0, 900, size=q_ub.size)
+    tile = int(rng.choice([8, 16, 32, 64, 128]))
+    items = make_prefill_items(q_ub, kv_ub, tile)
+    assert items.dtype == np.int32 and items.shape[1] == ops.PREFILL_ITEM_INTS
+    got = sorted((int(s), int(t)) for s, t in items[:, :2])
+    want = sorted((s, t) for s in range(q_ub.size) for t in range(0, int(q_ub[s]), tile))
+    assert got == want
+    cost = [int(kv_ub[s] - q_ub[s] + min(t + tile, q_ub[s])) for s, t in items[:, :2]]
+    assert all(a >= b for a, b in zip(cost, cost[1:])), "largest key count first"

@@ -1,0 +1,206 @@
+"""CPU: the oracle's floating-point functions pinned by mathematics.
+
+SiLU is checked against the closed form evaluated element by element with
+``math.exp`` and against torch's ``F.silu``; attention against pure-Python
+brute force on tiny inputs, against ``F.scaled_dot_product_attention`` on the
+cacheless causal case, and against invariants (one-key context, equal scores,
+split-K log-sum-exp merge).  Each check is chosen so that a plausible
+mistake fails it; the planted-mistake tests show that on the CPU.
+"""
+
+import json
+import math
+from pathlib import Path
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import reference as ref
+from tests._util import max_ulp_diff
+
+KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
+
+
+# ---------------------------------------------------------------------------
+# SiLU-and-mul
+# ---------------------------------------------------------------------------
+
+def _closed_form(x: torch.Tensor) -> torch.Tensor:
+    """g * sigmoid(g) * u per element in Python floats, rounded once."""
+    width = x.shape[-1] // 2
+    flat = x.float().reshape(-1, x.shape[-1]).tolist()
+    out = [[g / (1.0 + math.exp(-g)) * u for g, u in zip(row[:width], row[width:])] for row in flat]
+    return torch.tensor(out, dtype=torch.float64).reshape(*x.shape[:-1], width).to(x.dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", KATS["silu"]["shapes"])
+def test_silu_fused_matches_closed_form(dtype, shape):
+    gen = torch.Generator().manual_seed(7)
+    x = (torch.randn(shape, generator=gen) * 3).to(dtype)
+    fused = ref.silu_and_mul_fused(x)
+    assert fused.shape == (*shape[:-1], shape[-1] // 2) and fused.dtype == dtype
+    # fp32 arithmetic vs double: at most one unit of the last place apart.
+    assert max_ulp_diff(fused, _closed_form(x)) <= 1
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_silu_eager_is_torch_library_silu(dtype):
+    x = torch.randn(31, 64, generator=torch.Generator().manual_seed(3)).to(dtype)
+    a, b = x.chunk(2, -1)
+    assert torch.equal(ref.silu_and_mul_eager(x), F.silu(a) * b)
+    # Two roundings (eager) vs one (fused) differ by at most one ulp.
+    assert max_ulp_diff(ref.silu_and_mul_eager(x), ref.silu_and_mul_fused(x)) <= 1
+
+
+def test_silu_special_values():
+    x = torch.tensor([[0.0, -30.0, 30.0, 2.0, 5.0, 3.0]], dtype=torch.float32)
+    out = ref.silu_and_mul_fused(x)
+    # silu(0) = 0; silu(-30) ~ -2.8e-12; silu(30) ~ 30
+    assert out[0, 0].item() == 0.0
+    assert abs(out[0, 1].item()) < 1e-10
+    assert out[0, 2].item() == pytest.approx(90.0, rel=1e-6)
+
+
+def test_planted_silu_mistake_is_caught():
+    # A dropped sigmoid (g * u) must fail the closed-form check.
+    x = torch.randn(4, 16, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    a, b = x.float().chunk(2, -1)
+    wrong = (a * b).to(torch.bfloat16)
+    assert max_ulp_diff(wrong, _closed_form(x)) > 1
+
+
+# ---------------------------------------------------------------------------
+# Paged attention
+# ---------------------------------------------------------------------------
+
+def _brute_force_paged(q, k_cache, v_cache, block_tables, q_lens, kv_lens):
+    """Scalar loops: token (page, slot) lookup, causal bound, GQA head map."""
+    page = k_cache.shape[1]
+    hq, hkv, dim = q.shape[1], k_cache.shape[2], q.shape[2]
+    group = hq // hkv
+    scale = 1.0 / math.sqrt(dim)
+    out = torch.zeros(q.shape, dtype=torch.float64)
+    row = 0
+    for s, (ql, kl) in enumerate(zip(q_lens, kv_lens)):
+        for i in range(ql):
+            last = kl - ql + i  # absolute position of query i
+            for h in range(hq):
+                kvh = h // group
+                scores = []
+                for j in range(last + 1):
+                    pg = int(block_tables[s][j // page])
+                    kv = k_cache[pg, j % page, kvh]
+                    scores.append(sum(float(q[row, h, d]) * float(kv[d]) for d in range(dim)) * scale)
+                top = max(scores)
+                w = [math.exp(x - top) for x in scores]
+                total = sum(w)
+                for j in range(last + 1):
+                    pg = int(block_tables[s][j // page])
+                    for d in range(dim):
+                        out[row, h, d] += w[j] / total * float(v_cache[pg, j % page, kvh, d])
+            row += 1
+    return out
+
+
+def _tiny_case(seed, q_lens, kv_lens, hq, hkv, dim=8, page=4):
+    gen = torch.Generator().manual_seed(seed)
+    pages = sum((n + page - 1) // page for n in kv_lens) + 2
+    perm = torch.randperm(pages, generator=gen).tolist()
+    width = max((n + page - 1) // page for n in kv_lens)
+    bt, used = [], 0
+    for n in kv_lens:
+        c = (n + page - 1) // page
+        bt.append(perm[used : used + c] + [-1] * (width - c))
+        used += c
+    q = torch.randn(sum(q_lens), hq, dim, generator=gen)
+    k_cache = torch.randn(pages, page, hkv, dim, generator=gen)
+    v_cache = torch.randn(pages, page, hkv, dim, generator=gen)
+    return q, k_cache, v_cache, torch.tensor(bt), q_lens, kv_lens
+
+
+@pytest.mark.parametrize(
+    "q_lens,kv_lens,hq,hkv",
+    [([1, 1], [5, 9], 4, 2), ([3, 1], [7, 4], 4, 4), ([2, 3, 1], [2, 11, 6], 6, 2), ([4], [4], 2, 1)],
+)
+def test_paged_attention_matches_brute_force(q_lens, kv_lens, hq, hkv):
+    q, kc, vc, bt, ql, kl = _tiny_case(11, q_lens, kv_lens, hq, hkv)
+    got = ref.paged_attention(q, kc, vc, bt, ql, kl)
+    torch.testing.assert_close(got.double(), _brute_force_paged(q, kc, vc, bt, ql, kl), atol=1e-5, rtol=1e-5)
+
+
+def test_planted_causal_offset_mistake_is_caught():
+    # Queries aligned to the start of the context (a dropped kv - q offset)
+    # must fail the brute-force comparison.
+    q, kc, vc, bt, ql, kl = _tiny_case(5, [3], [7], 2, 1)
+    good = _brute_force_paged(q, kc, vc, bt, ql, kl)
+    wrong = _brute_force_paged(q, kc, vc, bt, ql, [3])  # offset 0: sees keys j <= i only
+    assert not torch.allclose(good, wrong, atol=1e-3)
+    torch.testing.assert_close(ref.paged_attention(q, kc, vc, bt, ql, kl).double(), good, atol=1e-5, rtol=1e-5)
+
+
+def test_planted_gqa_mapping_mistake_is_caught():
+    # Query head h reads KV head h // G; a tiled map (h % Hkv) must differ.
+    q, kc, vc, bt, ql, kl = _tiny_case(9, [1], [6], 4, 2)
+    got = ref.paged_attention(q, kc, vc, bt, ql, kl)
+    permuted = q.clone()
+    permuted[:, [1, 2]] = q[:, [2, 1]]  # swap heads across groups
+    tiled = ref.paged_attention(permuted, kc, vc, bt, ql, kl)[:, [0, 2, 1, 3]]
+    assert not torch.allclose(got, tiled, atol=1e-3)
+
+
+def test_one_key_context_returns_value_exactly():
+    q, kc, vc, bt, ql, kl = _tiny_case(2, [1, 1], [1, 1], 4, 2)
+    got = ref.paged_attention(q, kc, vc, bt, ql, kl)
+    for s in range(2):
+        expected = vc[int(bt[s][0]), 0].repeat_interleave(2, dim=0)
+        torch.testing.assert_close(got[s], expected, atol=0, rtol=0)
+
+
+def test_equal_scores_give_mean_of_values():
+    q, kc, vc, bt, ql, kl = _tiny_case(4, [1], [10], 2, 1)
+    q.zero_()
+    got = ref.paged_attention(q, kc, vc, bt, ql, kl)
+    keys = torch.cat([vc[int(p)] for p in bt[0][:3]])[:10]
+    torch.testing.assert_close(got[0], keys.mean(0).repeat_interleave(2, dim=0), atol=1e-6, rtol=1e-6)
+
+
+def test_ragged_attention_matches_sdpa():
+    gen = torch.Generator().manual_seed(13)
+    lengths = [3, 1, 6]
+    q = torch.randn(10, 4, 16, generator=gen)
+    k = torch.randn(10, 2, 16, generator=gen)
+    v = torch.randn(10, 2, 16, generator=gen)
+    got = ref.ragged_attention(q, k, v, lengths)
+    start = 0
+    for n in lengths:
+        qs = q[start : start + n].transpose(0, 1)
+        ks = k[start : start + n].repeat_interleave(2, dim=1).transpose(0, 1)
+        vs = v[start : start + n].repeat_interleave(2, dim=1).transpose(0, 1)
+        expected = F.scaled_dot_product_attention(qs, ks, vs, is_causal=True).transpose(0, 1)
+        torch.testing.assert_close(got[start : start + n], expected, atol=1e-5, rtol=1e-5)
+        start += n
+
+
+def test_paged_equals_ragged_when_context_is_the_query():
+    # A prefill with no cached prefix is the cacheless causal case.
+    q, kc, vc, bt, ql, kl = _tiny_case(21, [5, 3], [5, 3], 4, 2)
+    k = torch.cat([torch.cat([kc[int(p)] for p in bt[s][: (n + 3) // 4]])[:n] for s, n in enumerate(kl)])
+    v = torch.cat([torch.cat([vc[int(p)] for p in bt[s][: (n + 3) // 4]])[:n] for s, n in enumerate(kl)])
+    torch.testing.assert_close(ref.paged_attention(q, kc, vc, bt, ql, kl), ref.ragged_attention(q, k, v, kl),
+                               atol=1e-6, rtol=1e-6)
+
+
+@pytest.mark.parametrize("cuts", [[0, 37, 64], [0, 1, 2, 64], [0, 16, 32, 48, 64]])
+def test_split_k_lse_merge_equals_unsplit(cuts):
+    gen = torch.Generator().manual_seed(17)
+    qv = torch.randn(32, generator=gen)
+    keys = torch.randn(64, 32, generator=gen) * 2
+    values = torch.randn(64, 32, generator=gen)
+    scale = 32 ** -0.5
+    full, full_lse = ref.attention_partial(qv, keys, values, scale)
+    parts = [ref.attention_partial(qv, keys[a:b], values[a:b], scale) for a, b in zip(cuts, cuts[1:])]
+    merged = ref.lse_merge([o for o, _ in parts], [l for _, l in parts])
+    torch.testing.assert_close(merged, full, atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(torch.logsumexp(torch.stack([l for _, l in parts]), 0), full_lse)
