@@ -312,7 +312,7 @@ def make_decode_plan(
     first_q_row: int,
     num_kv_heads: int,
     num_waves: int,
-    pieces_per_wave: int = 4,
+    pieces_per_wave: float = 1.5,
     min_piece_pages: int = 4,
     max_piece_pages: int = ops.MAX_CHUNK_PAGES,
 ) -> tuple[np.ndarray, int, int]:
@@ -342,7 +342,7 @@ def make_decode_plan(
     seg_len = np.repeat(counts, num_kv_heads)
     nseg = seg_len.size
     total = int(seg_len.sum())
-    target = max(1, int(num_waves) * max(1, int(pieces_per_wave)))
+    target = max(1, int(num_waves * max(1.0, float(pieces_per_wave))))
     piece = int(np.clip(-(-total // target), min_piece_pages, max_piece_pages))
     nchunks = (seg_len + piece - 1) // piece
     seg_of = np.repeat(np.arange(nseg), nchunks)

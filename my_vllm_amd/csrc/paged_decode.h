@@ -98,9 +98,22 @@ __device__ inline float wave_sum16(float x) {
   return x + __shfl_xor(x, 32);
 }
 
+// Everything a split-K merge needs, passed by value: the merge is an
+// out-of-line call, so its registers do not add to the page loop's.
+struct MergeArgs {
+  float* part_lse;
+  float* part_o;
+  int32_t* counters;
+  void* out;
+  int64_t out_tok_stride;
+  int64_t out_head_stride;
+  int num_kv_heads;
+  int group;
+};
+
 template <typename T>
-__device__ inline void merge_partials(const DecodeParams& p, int s, int h, int pbase, int nchunks,
-                                      int64_t qrow, int lane, lds_u8* scratch);
+__device__ __attribute__((noinline)) void merge_partials(MergeArgs a, int s, int h, int pbase, int nchunks,
+                                                         int64_t qrow, lds_u8* scratch);
 
 // Scalar (SMEM) loads of data that is read-only for the whole launch (work
 // lists, page tables, lengths).  The constant address space tells the
@@ -285,6 +298,7 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
   const int C = min(kDecodeClaimCounters, W);
   const bool q_lane = c < G;
   int* const claim_ctr = p.sched + (wave % C) * kDecodeSchedLineInts;
+  const MergeArgs margs{p.part_lse, p.part_o, p.counters, p.out, p.out_tok_stride, p.out_head_stride, Hkv, G};
 
   // Descriptor fields: {seq, page_begin, page_end, chunk, n_chunks, part_base, q_row, kv_head}.
   auto desc_at = [&](int idx) -> i32x8 { return ((const_i32x8*)p.items)[idx]; };
@@ -352,7 +366,7 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
   const int voff = kDecodePageBytes + ((c >> 1) & 1) * 256 + (4 * q4 + (c >> 2)) * 16 + (c & 1) * 8;
 
   // `edge` pages contain tokens past seq_len; the choice is wave-uniform.
-  auto compute = [&](int pg, const lds_u8* buf, auto edge_tag) {
+  auto compute = [&](int pg, const lds_u8* buf, auto edge_tag) __attribute__((always_inline)) {
     constexpr bool edge = decltype(edge_tag)::value;
     f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -404,7 +418,7 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
 
   // End of piece X: the final output, or its split-K partial (normalised o
   // and log2-sum-exp, device-scope stores that go past this XCD's L2).
-  auto finish_piece = [&]() {
+  auto finish_piece = [&]() __attribute__((always_inline)) {
     const float l_tot = wave_sum16(l);
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
     const int h = X[7];
@@ -563,7 +577,7 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
     }
     if (merging) {
       const i32x8 D = desc_at(d_idx);
-      merge_partials<T>(p, D[0], D[7], D[5], D[4], D[6], lane, cur);
+      merge_partials<T>(margs, D[0], D[7], D[5], D[4], D[6], cur);
     }
     buf ^= 1;
     if (++i < np) continue;
@@ -609,7 +623,7 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
       int prev = 0;
       if (lane == 0) prev = __hip_atomic_fetch_add(p.counters + ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (__builtin_amdgcn_readfirstlane(prev) == D[4] - 1)
-        merge_partials<T>(p, D[0], D[7], D[5], D[4], D[6], lane, lds);
+        merge_partials<T>(margs, D[0], D[7], D[5], D[4], D[6], lds);
     }
   }
   if (lane == 0) {
@@ -641,8 +655,9 @@ constexpr int kLoadLdsDeviceScope = 16;
 // merge costs a few memory round trips whatever G is, without holding the
 // rows in registers.  Resets the arrival counter for the next launch.
 template <typename T>
-__device__ inline void merge_partials(const DecodeParams& p, int s, int h, int pbase, int nchunks,
-                                      int64_t qrow, int lane, lds_u8* scratch) {
+__device__ __attribute__((noinline)) void merge_partials(MergeArgs p, int s, int h, int pbase, int nchunks,
+                                                         int64_t qrow, lds_u8* scratch) {
+  const int lane = threadIdx.x & 63;
   const int G = p.group;
   const int Hkv = p.num_kv_heads;
   const float* lse_base = p.part_lse + ((int64_t)pbase * Hkv + h) * G;  // chunk k: + k*Hkv*G
