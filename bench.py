@@ -16,6 +16,10 @@ the CPU oracle (the reference's fp32 paged-attention restatement) on a
 bounded sample of the same workload on the host cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra]
+       python bench.py --only {decode,long_decode,prefill,mixed,silu,copy} [--steps K]
+The ``--only`` forms run one workload's kernel K times and print one line;
+they are the programs the committed rocprofv3 summaries profile (``copy`` is
+a 256 MiB device copy used to calibrate the byte counters).
 """
 
 from __future__ import annotations
@@ -40,6 +44,8 @@ def parse_args(argv=None):
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-extra", action="store_true", help="headline and roofline only")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
+    ap.add_argument("--only", choices=["decode", "long_decode", "prefill", "mixed", "silu", "copy"],
+                    help="run one workload's kernel --steps times (for profilers) and exit")
     return ap.parse_args(argv)
 
 
@@ -141,7 +147,7 @@ def headline(args, device):
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "kernel": "paged_decode_kernel<bf16>",
             "bytes_per_launch": dec_bytes,
             "avg_launch_ms": round(ms_decode, 5),
@@ -246,6 +252,84 @@ def extra_measurements(device, steps: int):
     return res
 
 
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "paged_decode_64seq_ctx128-2048_traffic.txt")
+
+
+def measured_traffic():
+    """HBM bytes per decode launch from the committed counter passes, or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch="):
+                    return int(line.split("=", 1)[1])
+    except OSError:
+        return None
+    return None
+
+
+def run_only(args, device):
+    """One workload's kernel, --steps launches, for rocprofv3 passes."""
+    from my_vllm_amd import ops
+    from my_vllm_amd.attention_backend import MI355XAttentionBackend
+    from my_vllm_amd.workloads import (config_decode_small, config_long_decode, config_mixed, config_prefill,
+                                       silu_input)
+
+    n = args.steps
+    if args.only == "copy":
+        a = torch.empty(256 << 20, dtype=torch.uint8, device=device)
+        b = torch.empty_like(a)
+        for _ in range(n):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"only": "copy", "bytes_read_per_launch": 256 << 20, "bytes_written_per_launch": 256 << 20,
+                          "launches": n}))
+        return 0
+    if args.only == "silu":
+        x = silu_input(4096, 6144, seed=0).to(device)
+        for _ in range(n):
+            ops.silu_and_mul(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"only": "silu", "bytes_per_launch": 75497472, "launches": n}))
+        return 0
+    if args.only in ("decode", "long_decode"):
+        if args.only == "decode":
+            batch, hq, hkv, copies = config_decode_small(seed=1), 16, 8, 4
+        else:
+            batch, hq, hkv, copies = config_long_decode(seed=4, device=device, rng_device="cuda"), 64, 8, 1
+        common = to_device(batch, device)
+        q = batch.q.to(device)
+        caches = [(batch.k_cache.to(device), batch.v_cache.to(device)) for _ in range(copies)]
+        backend = MI355XAttentionBackend(hq, hkv, 128, 16, torch.bfloat16)
+        md = backend.build_plan(common).metadata
+        out = torch.empty_like(q)
+        ws = backend._get_workspace(
+            ops.decode_workspace_bytes(common.num_seqs, md.num_decode_part_slots, hkv, hq // hkv), device)
+        for i in range(n):
+            kc, vc = caches[i % copies]
+            ops.paged_decode(q, kc, vc, md.block_tables, md.seq_lens, md.decode_items, md.num_decode_items,
+                             md.num_decode_waves, common.num_seqs, md.num_decode_part_slots, out, ws,
+                             backend.softmax_scale)
+        torch.cuda.synchronize()
+        print(json.dumps({"only": args.only, "bytes_per_launch": decode_bytes(batch, hq, hkv), "launches": n,
+                          "waves": md.num_decode_waves, "pieces": md.num_decode_items}))
+        return 0
+    batch = (config_prefill if args.only == "prefill" else config_mixed)(seed=2 if args.only == "prefill" else 3,
+                                                                        device=device, rng_device="cuda")
+    backend = MI355XAttentionBackend(32, 8, 128, 16, torch.bfloat16)
+    common = to_device(batch, device)
+    q = batch.q.to(device)
+    kc, vc = batch.k_cache.to(device), batch.v_cache.to(device)
+    plan = backend.build_plan(common)
+    empty = q.new_empty((0, 8, 128))
+    for _ in range(n):
+        backend.forward(q, empty, empty, kc, vc, plan)
+    torch.cuda.synchronize()
+    print(json.dumps({"only": args.only, "tokens": sum(batch.query_lengths), "launches": n,
+                      "route": plan.route.value}))
+    return 0
+
+
 def main(argv=None):
     args = parse_args(argv)
     if args.gpus != 1:
@@ -260,6 +344,8 @@ def main(argv=None):
     from my_vllm_amd import _native
 
     _native.load_library()  # fails loudly when the gfx950 library is missing
+    if args.only:
+        return run_only(args, device)
     head = headline(args, device)
     extra = {} if args.no_extra else extra_measurements(device, args.steps)
     cpu = cpu_baseline(head["batch"], args.cpu_seconds)
