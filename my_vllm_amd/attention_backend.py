@@ -558,12 +558,17 @@ class MI355XAttentionBackendMixin:
         num_decode_waves = 0
         num_part_slots = 0
         if common.num_decode_seqs:
+            waves = resident_decode_waves(block_tables.device)
+            if common.num_prefill_seqs and self.attention_mode == "unified":
+                # One MIXED launch: leave a quarter of the wave slots to the
+                # prefill tiles from the start, so they overlap the decode stream.
+                waves = max(1, waves * 3 // 4)
             items, num_decode_waves, num_part_slots = make_decode_plan(
                 counts[common.num_prefill_seqs:],
                 common.num_prefill_seqs,
                 common.num_prefill_tokens,
                 self.num_kv_heads,
-                resident_decode_waves(block_tables.device),
+                waves,
             )
             num_decode_items = items.shape[0]
             decode_items = _to_device(items, block_tables.device)

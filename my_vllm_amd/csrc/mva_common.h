@@ -121,6 +121,39 @@ __device__ inline void lds_ld_tr16_x8_stride512(const lds_u8* base, s16x4 (&out)
       : "memory");
 }
 
+// Four 1 KB global -> LDS copies from a uniform base: copy c moves 16 bytes
+// per lane from base + 64*c + voff to LDS byte address lds + 1024*c + 16*lane.
+// Written as one asm block so the scalar base + 32-bit lane offset form is
+// used (no 64-bit per-lane addresses) and M0 is restored afterwards.  The
+// instruction's immediate offset would also move the LDS destination, so each
+// copy gets its own scalar base instead.  The s_nop after each M0 write is
+// the wait state an LDS DMA needs after an SALU write of M0.  The compiler
+// does not track these loads: callers wait for them (vmcnt) and synchronize
+// before reading the LDS they fill.
+__device__ inline void dma16_x4_saddr(const void* base, uint32_t voff, uint32_t lds) {
+  uint32_t m0_saved;
+  const char* b = (const char*)base;
+  lds = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile(
+      "s_mov_b32 %[m0s], m0\n\t"
+      "s_mov_b32 m0, %[l]\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %[vo], %[b0]\n\t"
+      "s_add_u32 m0, %[l], 0x400\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %[vo], %[b1]\n\t"
+      "s_add_u32 m0, %[l], 0x800\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %[vo], %[b2]\n\t"
+      "s_add_u32 m0, %[l], 0xc00\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %[vo], %[b3]\n\t"
+      "s_mov_b32 m0, %[m0s]"
+      : [m0s] "=&s"(m0_saved)
+      : [l] "s"(lds), [vo] "v"(voff), [b0] "s"(b), [b1] "s"(b + 64), [b2] "s"(b + 128), [b3] "s"(b + 192)
+      : "memory", "scc");
+}
+
 // 16-byte global -> LDS copy; lane i's bytes land at lds_base + 16*i.
 __device__ inline void dma16(const void* g, lds_u8* lds_base) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);

@@ -194,20 +194,28 @@ __device__ inline void decode_step(DecodeStepIo& io, int claiming, int arriving,
         "s_mov_b64 exec, %[sv]\n\t"
         "s_mov_b32 %[m0s], m0\n\t"
         "s_mov_b32 m0, %[lv]\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dwordx4 %[v0], off\n\t"
         "s_add_u32 m0, %[lv], 0x400\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dwordx4 %[v1], off\n\t"
         "s_add_u32 m0, %[lv], 0x800\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dwordx4 %[v2], off\n\t"
         "s_add_u32 m0, %[lv], 0xc00\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dwordx4 %[v3], off\n\t"
         "s_mov_b32 m0, %[lk]\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dwordx4 %[k0], off\n\t"
         "s_add_u32 m0, %[lk], 0x400\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dwordx4 %[k1], off\n\t"
         "s_add_u32 m0, %[lk], 0x800\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dwordx4 %[k2], off\n\t"
         "s_add_u32 m0, %[lk], 0xc00\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dwordx4 %[k3], off\n\t"
         "s_mov_b32 m0, %[m0s]\n\t"
         "s_waitcnt vmcnt(8)"

@@ -14,15 +14,19 @@
 // so every K/V byte staged in LDS serves all G heads.  Wave w owns rows
 // 32w .. 32w + 31.
 //
-// Per 64-key tile (double-buffered in LDS, filled by global_load_lds):
+// Per 64-key tile t, the K and V tiles sit in separate double-buffered LDS
+// arrays, filled by global_load_lds:
 //   S^T[key, q] = K[key, :] . Q[q, :]       v_mfma_f32_32x32x16 (A = K from LDS,
 //                                            B = Q held in registers)
 //   online softmax per query (each lane owns one query row: the C layout of
 //   S^T puts a query's 32 keys in lanes l and l^32)
 //   O^T[d, q] += V^T[d, key] P^T[key, q]    (A = V^T via ds_read_b64_tr_b16,
 //                                            B = P^T straight from S^T's C layout)
-// The running max is only moved when it grows by more than 8 (log2 units), so
-// the O rescale is skipped on most tiles.
+// Software pipeline: iteration t computes S(t+1) on the matrix cores while
+// the vector ALUs run the softmax of S(t), then accumulates P(t) V(t).  K runs
+// one tile ahead of V, so iteration t needs K(t+1) and V(t) resident while
+// K(t+2) and V(t+1) stream in.  The running max is only moved when it grows
+// by more than 8 (log2 units), so the O rescale is skipped on most tiles.
 #pragma once
 
 #include "mva_common.h"
@@ -33,8 +37,6 @@ namespace mva {
 constexpr int kPrefillRows = 128;  // query rows per workgroup
 constexpr int kPrefillKeys = 64;   // keys per LDS tile
 constexpr int kPrefillTileBytes = kPrefillKeys * kHeadDim * 2;  // one K (or V) tile
-constexpr int kPrefillPtabEntries = 2048;                       // page ids staged per segment
-constexpr int kPrefillLdsBytes = 4 * kPrefillTileBytes + kPrefillPtabEntries * 4;
 constexpr int kPrefillItemInts = 4;  // {seq, first token of the tile, 0, 0}
 
 struct PrefillParams {
@@ -76,11 +78,28 @@ __device__ inline int vlds_blk_off(int key, int ch) {
   return (((key >> 4) << 2) + (ch >> 2)) * 1024 + (key & 15) * 64 + (ch & 3) * 16;
 }
 
+// Max / sum of a value over the lane pair (l, l ^ 32): v_permlane32_swap
+// exchanges the two 32-lane halves without going through LDS.
+__device__ inline float pair_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float pair_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// One prefill work item.  k0/k1 and v0/v1 must be four distinct __shared__
+// arrays of kPrefillTileBytes: with distinct objects the compiler can tell
+// that a DMA into one buffer does not alias reads of another and does not
+// wait for in-flight DMAs before every LDS read.
 template <typename T>
-__device__ void prefill_item(const PrefillParams& p, const int32_t* __restrict__ it, int h, lds_u8* lds) {
+__device__ __attribute__((always_inline)) inline void prefill_item(
+    const PrefillParams& p, const int32_t* __restrict__ it, int h, lds_u8* k0, lds_u8* k1, lds_u8* v0,
+    lds_u8* v1) {
   typedef typename Elem<T>::v8 V8;
   const int tid = threadIdx.x;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int ln = lane & 31;
   const int hi = lane >> 5;
@@ -105,13 +124,7 @@ __device__ void prefill_item(const PrefillParams& p, const int32_t* __restrict__
   const int t_end = min(t0 + BMT, q_len);
   const int kv_end = base_pos + t_end;  // keys [0, kv_end) are needed by some row
   const int ntiles = (kv_end + kPrefillKeys - 1) / kPrefillKeys;
-  const int full_tiles = (base_pos + t0 + 1) / kPrefillKeys;  // tiles no row masks
-
-  // LDS: K buffers at [0, 32K), V buffers at [32K, 64K), page ids after.
-  auto kbuf = [&](int b) { return lds + b * kPrefillTileBytes; };
-  auto vbuf = [&](int b) { return lds + (2 + b) * kPrefillTileBytes; };
-  __attribute__((address_space(3))) int32_t* ptab =
-      reinterpret_cast<__attribute__((address_space(3))) int32_t*>(lds + 4 * kPrefillTileBytes);
+  const int full_tiles = min((base_pos + t0 + 1) / kPrefillKeys, ntiles);  // tiles no row masks
 
   // Q fragments (B operand of S^T = K Q^T): k-step kk covers d-chunk 2*kk + hi.
   V8 qf[8];
@@ -128,32 +141,34 @@ __device__ void prefill_item(const PrefillParams& p, const int32_t* __restrict__
   const int32_t* bt = p.block_tables + (int64_t)s * p.bt_stride;
   const int npages = (kv_end + kPageSize - 1) / kPageSize;
 
-  // Stage page ids [seg0, seg0 + 2048) of this sequence in LDS.
-  auto load_ptab = [&](int seg0) {
-    for (int i = tid; i < kPrefillPtabEntries && seg0 + i < npages; i += 256) {
-      int pg = bt[seg0 + i];
-      ptab[i] = (pg >= 0 && pg < p.num_pages) ? pg : 0;
-    }
+  // Page id of this wave's page (page w of the 4 in a tile) of `tile`; pages
+  // past the needed range clamp to the last needed page (masked later).
+  auto page_of = [&](int tile) {
+    const int pg = sload(bt, min(tile * (kPrefillKeys / kPageSize) + w, npages - 1));
+    return (pg >= 0 && pg < p.num_pages) ? pg : 0;
   };
-  int seg0 = 0;
-  load_ptab(0);
-  __syncthreads();
+  // DMA of this wave's page of a K (or V) tile: 4 blocks of 1 KB.  Source =
+  // uniform page base + a 32-bit per-lane byte offset (+ 64 bytes per block).
+  //   K block cg: lane -> token lane%16, chunk 4*cg + lane/16
+  //   V block cg: lane -> token lane/4,  chunk 4*cg + lane%4
+  const uint32_t koff = (uint32_t)(((lane & 15) * p.tok_stride + 8 * (lane >> 4)) * (int64_t)sizeof(T));
+  const uint32_t voff = (uint32_t)(((lane >> 2) * p.tok_stride + 8 * (lane & 3)) * (int64_t)sizeof(T));
+  auto dma_k = [&](int page, lds_u8* buf) {
+    dma16_x4_saddr(kc + (int64_t)page * p.page_stride, koff, (uint32_t)(uintptr_t)(buf + 4096 * w));
+  };
+  auto dma_v = [&](int page, lds_u8* buf) {
+    dma16_x4_saddr(vc + (int64_t)page * p.page_stride, voff, (uint32_t)(uintptr_t)(buf + 4096 * w));
+  };
 
-  // DMA of tile `tile` into buffer `b`: wave w loads page w of the tile (16
-  // keys): 4 K blocks and 4 V blocks of 1 KB.  Keys past the needed range
-  // clamp to the last needed page and are masked later.
-  auto load_tile = [&](int tile, int b) {
-    const int pg_abs = min(tile * (kPrefillKeys / kPageSize) + w, npages - 1);
-    const int page = ptab[pg_abs - seg0];  // tiles never straddle a segment
-    const T* kp = kc + (int64_t)page * p.page_stride;
-    const T* vp = vc + (int64_t)page * p.page_stride;
+  // S^T of one tile: st[mt][i] = S[query ln][key 32*mt + 8*(i/4) + 4*hi + i%4].
+  auto qk = [&](const lds_u8* kb, f32x16 (&st)[2]) {
 #pragma unroll
-    for (int cg = 0; cg < 4; ++cg) {
-      const int blk = 4 * w + cg;
-      // K block: lane -> token lane%16, chunk 4*cg + lane/16.
-      dma16(kp + (lane & 15) * p.tok_stride + 8 * (4 * cg + (lane >> 4)), kbuf(b) + blk * 1024);
-      // V block: lane -> token lane/4, chunk 4*cg + lane%4.
-      dma16(vp + (lane >> 2) * p.tok_stride + 8 * (4 * cg + (lane & 3)), vbuf(b) + blk * 1024);
+    for (int mt = 0; mt < 2; ++mt) {
+      st[mt] = f32x16{};
+      const int key = 32 * mt + ln;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk)
+        st[mt] = Elem<T>::mfma32(lds_ld16<V8>(kb + klds_off(key, 2 * kk + hi)), qf[kk], st[mt]);
     }
   };
 
@@ -163,24 +178,11 @@ __device__ void prefill_item(const PrefillParams& p, const int32_t* __restrict__
   float m = -INFINITY;
   float l = 0.f;
 
-  auto compute = [&](int tile, int b, auto masked_tag) {
+  // Softmax of S(t): P fragments for the PV k-steps and the O rescale factor.
+  // Returns whether any lane must rescale O before P(t) V(t) accumulates.
+  auto softmax = [&](int tile, f32x16 (&st)[2], V8 (&pf)[4], float& alpha, auto masked_tag) {
     constexpr bool masked = decltype(masked_tag)::value;
-    const lds_u8* kb = kbuf(b);
-    const lds_u8* vb = vbuf(b);
     const int j0 = tile * kPrefillKeys;
-    f32x16 st[2];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      st[mt] = f32x16{};
-      const int key = 32 * mt + ln;
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const V8 a = lds_ld16<V8>(kb + klds_off(key, 2 * kk + hi));
-        st[mt] = Elem<T>::mfma32(a, qf[kk], st[mt]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    // st[mt][i] = S[query ln][key j0 + 32*mt + 8*(i/4) + 4*hi + i%4]
     float tmax = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
@@ -192,83 +194,115 @@ __device__ void prefill_item(const PrefillParams& p, const int32_t* __restrict__
         }
         tmax = fmaxf(tmax, st[mt][i]);
       }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float tmax_s = tmax * p.scale_log2;  // scale > 0 commutes with max
+    const float tmax_s = pair_max(tmax) * p.scale_log2;  // scale > 0 commutes with max
     // Move the reference max only when it grows by > 8 (p stays <= 2^8).
     const bool grow = tmax_s > m + 8.0f;
-    if (__any(grow)) {
-      const float m_new = grow ? tmax_s : m;
-      const float alpha = grow ? fast_exp2(m - m_new) : 1.0f;  // m = -inf -> 0
-      m = m_new;
-      l *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
-    }
+    const float m_new = grow ? tmax_s : m;
+    alpha = grow ? fast_exp2(m - m_new) : 1.0f;  // m = -inf -> 0
+    m = m_new;
+    l *= alpha;
     const float m_use = (m == -INFINITY) ? 0.f : m;
-    V8 pf[4];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const float pr = fast_exp2(st[mt][i] * p.scale_log2 - m_use);
         l += pr;
-        // PV k-step kk = 2*mt + (i/4)/2 takes blocks b0 = 2*(kk%2), b0+1:
-        // slot (i/4 % 2)*4 + i%4.
+        // PV k-step kk = 2*mt + (i/4)/2, slot (i/4 % 2)*4 + i%4.
         pf[2 * mt + ((i >> 2) >> 1)][((i >> 2) & 1) * 4 + (i & 3)] = (T)pr;
       }
-    // PV: A = V^T via transposed LDS reads.  16-lane group a = lane/16 covers
-    // d offset 16*(a&1) of the 32-d tile and keys 4*hi.. of each 8-key block;
-    // supplier lane ti gives row 4*hi + ti/4 at d offset 4*(ti%4).
-    const int ti = lane & 15;
-    const int dgrp = (lane >> 4) & 1;
-    const lds_u8* vlane = vb + (4 * hi + (ti >> 2)) * 64 + (2 * dgrp + ((ti >> 1) & 1)) * 16 + (ti & 1) * 8;
+    return __any(grow);
+  };
+
+  // PV: A = V^T via transposed LDS reads.  16-lane group a = lane/16 covers
+  // d offset 16*(a&1) of the 32-d tile and keys 4*hi.. of each 8-key block;
+  // supplier lane ti gives row 4*hi + ti/4 at d offset 4*(ti%4).  The reads
+  // for (dt, j) of k-step kk sit at byte dt*1024 + j*512 past block 4*kk.
+  const int ti = lane & 15;
+  const int dgrp = (lane >> 4) & 1;
+  const int vlane_off = (4 * hi + (ti >> 2)) * 64 + (2 * dgrp + ((ti >> 1) & 1)) * 16 + (ti & 1) * 8;
+  auto pv = [&](const lds_u8* vb, const V8 (&pf)[4]) {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      // Reads for (dt, j) sit at byte dt*1024 + j*512 past block 4*kk.
-      s16x4 vt[8];
-      lds_ld_tr16_x8_stride512(vlane + 4 * kk * 1024, vt);
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const s16x8 both = __builtin_shufflevector(vt[2 * dt], vt[2 * dt + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+        const lds_u8* a = vb + vlane_off + 4 * kk * 1024 + dt * 1024;
+        const s16x4 lo = lds_ld_tr16(a);
+        const s16x4 up = lds_ld_tr16(a + 512);
+        const s16x8 both = __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7);
         o[dt] = Elem<T>::mfma32(__builtin_bit_cast(V8, both), pf[kk], o[dt]);
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
   // Zero V rows of keys >= kv in the last tile (stale rows may hold NaN and
   // 0 * NaN would leak through P = 0).
-  auto zero_tail = [&](int tile, int b) {
+  auto zero_tail = [&](int tile, lds_u8* vb) {
     const int first_bad = kv - tile * kPrefillKeys;  // rows >= first_bad are past the sequence
-    if (first_bad >= kPrefillKeys) return;
     for (int i = tid; i < (kPrefillKeys - first_bad) * 16; i += 256) {
       const int key = first_bad + (i >> 4);
-      lds_st16<u32x4>(vbuf(b) + vlds_blk_off(key, i & 15), u32x4{0, 0, 0, 0});
+      lds_st16<u32x4>(vb + vlds_blk_off(key, i & 15), u32x4{0, 0, 0, 0});
     }
   };
 
-  load_tile(0, 0);
-  for (int tile = 0; tile < ntiles; ++tile) {
-    const int b = tile & 1;
-    __builtin_amdgcn_s_waitcnt(kVmcnt0);
-    __syncthreads();  // tile landed for all waves; the other buffer is free
-    if ((tile + 1) * kPrefillKeys / kPageSize - seg0 >= kPrefillPtabEntries && tile + 1 < ntiles) {
-      // Next tile starts past the staged page ids: restage (rare, > 32K keys).
-      seg0 = (tile + 1) * kPrefillKeys / kPageSize;
-      load_ptab(seg0);
-      __syncthreads();
-    }
-    if (tile + 1 < ntiles) load_tile(tile + 1, b ^ 1);
-    if (tile == ntiles - 1 && (tile + 1) * kPrefillKeys > kv) {
-      zero_tail(tile, b);
-      __syncthreads();
-    }
-    if (tile < full_tiles) compute(tile, b, std::false_type{});
-    else compute(tile, b, std::true_type{});
+  // Prologue: K(0), K(1), V(0) in flight, then S(0).
+  int pg_v = page_of(1);   // page of V(t+1) at iteration t (= page of K(t+1))
+  int pg_k = page_of(2);   // page of K(t+2) at iteration t
+  {
+    const int pg0 = page_of(0);
+    dma_k(pg0, k0);
+    if (ntiles > 1) dma_k(pg_v, k1);
+    dma_v(pg0, v0);
   }
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);
+  __syncthreads();
+  f32x16 st_cur[2];
+  qk(k0, st_cur);
+
+  // Iteration t.  kb_cur holds K(t) (free: S(t) is done) and receives
+  // K(t+2); kb_next holds K(t+1); vb_cur holds V(t); vb_next receives V(t+1).
+  auto iteration = [&](int t, lds_u8* kb_cur, lds_u8* kb_next, lds_u8* vb_cur, lds_u8* vb_next,
+                       auto masked_tag) {
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    __syncthreads();  // K(t+1), V(t) landed for all waves; S(t) and PV(t-1) done everywhere
+    if (t == ntiles - 1 && (t + 1) * kPrefillKeys > kv) {
+      zero_tail(t, vb_cur);
+      __syncthreads();
+    }
+    if (t + 2 < ntiles) dma_k(pg_k, kb_cur);
+    if (t + 1 < ntiles) dma_v(pg_v, vb_next);
+    pg_v = pg_k;
+    pg_k = page_of(t + 3);
+    // S(t+1) on the matrix cores alongside the softmax of S(t).  Past the
+    // last tile this reads a stale buffer and the result is never used.
+    f32x16 st_next[2];
+    qk(kb_next, st_next);
+    V8 pf[4];
+    float alpha;
+    if (softmax(t, st_cur, pf, alpha, masked_tag)) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+    }
+    pv(vb_cur, pf);
+    st_cur[0] = st_next[0];
+    st_cur[1] = st_next[1];
+  };
+
+  // Tiles below every row's causal bound, then the masked diagonal tiles.
+  // Unrolled by two so each iteration body names its LDS buffers statically.
+  auto run = [&](int t, int t_stop, auto masked_tag) {
+    if (t < t_stop && (t & 1)) iteration(t++, k1, k0, v1, v0, masked_tag);
+    for (; t + 1 < t_stop; t += 2) {
+      iteration(t, k0, k1, v0, v1, masked_tag);
+      iteration(t + 1, k1, k0, v1, v0, masked_tag);
+    }
+    if (t < t_stop) iteration(t, k0, k1, v0, v1, masked_tag);
+  };
+  run(0, full_tiles, std::false_type{});
+  run(full_tiles, ntiles, std::true_type{});
 
   // Epilogue: O^T / l -> out[token][head][d].
-  const float l_tot = l + __shfl_xor(l, 32);
+  const float l_tot = pair_sum(l);
   if (!row_ok) return;
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
   T* op = (T*)p.out + (int64_t)(q0 + tq) * p.out_tok_stride + (int64_t)(h * G + g) * p.out_head_stride;

@@ -20,31 +20,63 @@ namespace {
 template <typename T>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void paged_prefill_kernel(
     PrefillParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kPrefillLdsBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t k0[kPrefillTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t k1[kPrefillTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t v0[kPrefillTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t v1[kPrefillTileBytes];
   const int h = (int)(blockIdx.x % (uint32_t)p.num_kv_heads);
   const int item = (int)(blockIdx.x / (uint32_t)p.num_kv_heads);
-  prefill_item<T>(p, p.items + (int64_t)item * kPrefillItemInts, h, (lds_u8*)lds);
+  prefill_item<T>(p, p.items + (int64_t)item * kPrefillItemInts, h, (lds_u8*)k0, (lds_u8*)k1, (lds_u8*)v0,
+                  (lds_u8*)v1);
 }
 
-// Workgroups [0, n_prefill_wgs) run prefill tiles; the rest run four decode
-// (item, KV head) pairs each, one per wavefront, with private LDS buffers.
+// Workgroup roles of the MIXED launch: the decode workgroups come first, in
+// chunks of 8 blocks (blocks are dealt to the 8 XCDs round-robin), then the
+// prefill workgroups.  The host sizes the decode part below the GPU's
+// resident capacity, so every decode wavefront starts at once and prefill
+// tiles fill the remaining slots (and the slots decode frees): HBM-bound
+// decode streaming overlaps MFMA-bound prefill on the same CUs.  Prefill
+// blocks keep index % 8 == block % 8, so a prefill work item's KV head
+// (index % num_kv_heads) stays on the same XCD as in the prefill-only launch.
+struct MixedRole {
+  bool prefill;
+  uint32_t index;  // prefill workgroup or decode workgroup number
+};
+__host__ __device__ inline uint32_t mixed_chunks(uint32_t n) { return (n + 7u) >> 3; }
+__device__ inline MixedRole mixed_role(uint32_t block, uint32_t n_decode_wgs) {
+  const uint32_t c = block >> 3, r = block & 7u;
+  const uint32_t cd = mixed_chunks(n_decode_wgs);
+  if (c < cd) return {false, c * 8u + r};
+  return {true, (c - cd) * 8u + r};
+}
+
+// Prefill workgroups run prefill tiles; decode workgroups run four decode
+// wavefronts each, with private LDS buffers.
 template <typename T>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void paged_mixed_kernel(
-    PrefillParams pp, DecodeParams dp, uint32_t n_prefill_wgs) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kPrefillLdsBytes];
-  if (blockIdx.x < n_prefill_wgs) {
-    const int h = (int)(blockIdx.x % (uint32_t)pp.num_kv_heads);
-    const int item = (int)(blockIdx.x / (uint32_t)pp.num_kv_heads);
-    prefill_item<T>(pp, pp.items + (int64_t)item * kPrefillItemInts, h, (lds_u8*)lds);
+    PrefillParams pp, DecodeParams dp, uint32_t n_prefill_wgs, uint32_t n_decode_wgs) {
+  __shared__ __attribute__((aligned(16))) uint8_t k0[kPrefillTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t k1[kPrefillTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t v0[kPrefillTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t v1[kPrefillTileBytes];
+  const MixedRole role = mixed_role(blockIdx.x, n_decode_wgs);
+  if (role.prefill) {
+    if (role.index >= n_prefill_wgs) return;
+    const int h = (int)(role.index % (uint32_t)pp.num_kv_heads);
+    const int item = (int)(role.index / (uint32_t)pp.num_kv_heads);
+    prefill_item<T>(pp, pp.items + (int64_t)item * kPrefillItemInts, h, (lds_u8*)k0, (lds_u8*)k1,
+                    (lds_u8*)v0, (lds_u8*)v1);
     return;
   }
   const int w = threadIdx.x >> 6;
-  const int64_t wave = (int64_t)(blockIdx.x - n_prefill_wgs) * 4 + w;
+  const int64_t wave = (int64_t)role.index * 4 + w;
   if (wave >= dp.num_waves) return;
-  decode_wave<T>(dp, (int)wave, (lds_u8*)lds + w * kDecodeWaveLdsBytes);
+  // Each decode wavefront gets one of the four prefill buffers.
+  lds_u8* mine = (lds_u8*)(w == 0 ? k0 : w == 1 ? k1 : w == 2 ? v0 : v1);
+  decode_wave<T>(dp, (int)wave, mine);
 }
 
-static_assert(4 * kDecodeWaveLdsBytes <= kPrefillLdsBytes, "decode buffers must fit the prefill LDS");
+static_assert(kDecodeWaveLdsBytes <= kPrefillTileBytes, "a decode wave's buffers must fit one prefill buffer");
 
 }  // namespace
 
@@ -153,14 +185,15 @@ extern "C" int mva_paged_mixed(const void* q, int64_t q_token_stride, int64_t q_
   if (rc) return rc;
   const int64_t n_prefill_wgs = num_prefill_items * num_kv_heads;
   const int64_t n_decode_wgs = num_decode_items > 0 ? (num_decode_waves + 3) / 4 : 0;
-  if (n_prefill_wgs + n_decode_wgs > 0x7fffffffLL) return set_error("paged attention: too many work items");
+  if (n_prefill_wgs + n_decode_wgs > 0x7fffff00LL) return set_error("paged attention: too many work items");
   if (n_prefill_wgs + n_decode_wgs == 0) return 0;
-  const dim3 grid((uint32_t)(n_prefill_wgs + n_decode_wgs));
+  const uint32_t np = (uint32_t)n_prefill_wgs, nd = (uint32_t)n_decode_wgs;
+  const dim3 grid(8u * (mixed_chunks(np) + mixed_chunks(nd)));
   hipStream_t s = (hipStream_t)stream;
   if (dtype == kBF16)
-    hipLaunchKernelGGL(paged_mixed_kernel<__bf16>, grid, dim3(256), 0, s, pp, dp, (uint32_t)n_prefill_wgs);
+    hipLaunchKernelGGL(paged_mixed_kernel<__bf16>, grid, dim3(256), 0, s, pp, dp, np, nd);
   else if (dtype == kF16)
-    hipLaunchKernelGGL(paged_mixed_kernel<_Float16>, grid, dim3(256), 0, s, pp, dp, (uint32_t)n_prefill_wgs);
+    hipLaunchKernelGGL(paged_mixed_kernel<_Float16>, grid, dim3(256), 0, s, pp, dp, np, nd);
   else return set_error("paged attention: dtype must be bf16 or fp16");
   return check_launch("paged_mixed");
 }
