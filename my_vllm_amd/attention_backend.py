@@ -379,8 +379,11 @@ def make_prefill_items(
 
     ``query_upper[s]`` bounds the sequence's new-token count (exact when known;
     tiles past the real count exit on the device) and ``kv_upper[s]`` its
-    context length.  Tiles are ordered by their estimated key count, largest
-    first, so long causal rows start early.
+    context length.  Tiles are grouped by sequence, longest context first, and
+    within a sequence ordered by their key count, largest first.  Grouping
+    keeps the tiles that read one sequence's K/V in flight together, so
+    those pages are served from L2 instead of being refetched for tiles of
+    many sequences at once; longest-first keeps the launch's tail short.
     """
     q_ub = np.asarray(query_upper, dtype=np.int64)
     kv_ub = np.asarray(kv_upper, dtype=np.int64)
@@ -394,7 +397,9 @@ def make_prefill_items(
     items = np.zeros((seq.size, ops.PREFILL_ITEM_INTS), dtype=np.int32)
     items[:, 0] = seq
     items[:, 1] = start
-    order = np.argsort(-cost, kind="stable")
+    # Primary key: the sequence's context (longest first, ties by index);
+    # secondary: the tile's key count (largest first).
+    order = np.lexsort((-cost, seq, -kv_ub[seq]))
     return items[order]
 
 

@@ -100,6 +100,12 @@ __device__ inline float wave_sum16(float x) {
 
 // Everything a split-K merge needs, passed by value: the merge is an
 // out-of-line call, so its registers do not add to the page loop's.
+// Partial rows (512 bytes each) the merge stages in LDS at once: one page
+// buffer inside the page loop (the other may hold an in-flight DMA), both at
+// the wavefront's exit.
+constexpr int kMergeRowsInLoop = 2 * kDecodePageBytes / 512;
+constexpr int kMergeRowsAtExit = 4 * kDecodePageBytes / 512;
+
 struct MergeArgs {
   float* part_lse;
   float* part_o;
@@ -113,7 +119,7 @@ struct MergeArgs {
 
 template <typename T>
 __device__ __attribute__((noinline)) void merge_partials(MergeArgs a, int s, int h, int pbase, int nchunks,
-                                                         int64_t qrow, lds_u8* scratch);
+                                                         int64_t qrow, lds_u8* scratch, int scratch_rows);
 
 // Scalar (SMEM) loads of data that is read-only for the whole launch (work
 // lists, page tables, lengths).  The constant address space tells the
@@ -585,7 +591,7 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
     }
     if (merging) {
       const i32x8 D = desc_at(d_idx);
-      merge_partials<T>(margs, D[0], D[7], D[5], D[4], D[6], cur);
+      merge_partials<T>(margs, D[0], D[7], D[5], D[4], D[6], cur, kMergeRowsInLoop);
     }
     buf ^= 1;
     if (++i < np) continue;
@@ -631,7 +637,7 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
       int prev = 0;
       if (lane == 0) prev = __hip_atomic_fetch_add(p.counters + ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (__builtin_amdgcn_readfirstlane(prev) == D[4] - 1)
-        merge_partials<T>(margs, D[0], D[7], D[5], D[4], D[6], lds);
+        merge_partials<T>(margs, D[0], D[7], D[5], D[4], D[6], lds, kMergeRowsAtExit);
     }
   }
   if (lane == 0) {
@@ -656,30 +662,60 @@ constexpr int kLoadLdsDeviceScope = 16;
 // Merges the n_chunks split-K partials of (sequence s, KV head h) into the
 // output rows of its G query heads:
 //   o = sum_k w_k o_k / sum_k w_k,  w_k = 2^(lse_k - max_k lse_k).
-// Lane L owns chunks L, L+64, ... in the log-sum-exp passes and output
-// columns d = 2L, 2L+1 in the weighted sum.  The partial rows of up to 16
-// (chunk, head) pairs at a time are copied into `scratch` (8 KB of the
-// wavefront's LDS) with coherent global_load_lds and summed from there, so a
-// merge costs a few memory round trips whatever G is, without holding the
-// rows in registers.  Resets the arrival counter for the next launch.
+// Lane L owns chunks L, L+64, ... in the log-sum-exp pass and output columns
+// d = 2L, 2L+1 in the weighted sum.  The partial rows of up to scratch_rows /
+// G chunks at a time are copied into `scratch` with coherent global_load_lds
+// and summed from there, without holding the rows in registers.  The first
+// batch of rows is requested together with the log-sum-exps, so a merge of
+// up to scratch_rows / G chunks costs one memory round trip.  Resets the
+// arrival counter for the next launch.
 template <typename T>
 __device__ __attribute__((noinline)) void merge_partials(MergeArgs p, int s, int h, int pbase, int nchunks,
-                                                         int64_t qrow, lds_u8* scratch) {
+                                                         int64_t qrow, lds_u8* scratch, int scratch_rows) {
   const int lane = threadIdx.x & 63;
   const int G = p.group;
   const int Hkv = p.num_kv_heads;
   const float* lse_base = p.part_lse + ((int64_t)pbase * Hkv + h) * G;  // chunk k: + k*Hkv*G
   const int64_t lse_chunk = (int64_t)Hkv * G;
-  float mx[16];
-#pragma unroll
-  for (int g = 0; g < 16; ++g) mx[g] = -INFINITY;
-  for (int k0 = 0; k0 < nchunks; k0 += 64) {
-    // Clamped chunk index: a repeated chunk leaves the maximum unchanged.
+  // A chunk's G rows are contiguous (G * 512 bytes); `batch` chunks fill at
+  // most scratch_rows rows of scratch, counting the spare row an odd G's last
+  // row pair writes.
+  const int batch = max(1, (scratch_rows - (G & 1)) / G);
+  const int64_t o_chunk = (int64_t)Hkv * G * kHeadDim;
+  const float* o_base = p.part_o + ((int64_t)pbase * Hkv + h) * G * kHeadDim;
+  const int pairs = (G + 1) / 2;  // 1 KB copies per chunk (two rows each)
+  const int d = 2 * lane;
+  // Row pair (2q, 2q+1) of chunk k + b lands at scratch + (b*G + 2q)*512;
+  // lanes 32..63 of an odd G's last pair re-read row 2q (in bounds) into the
+  // next row slot, which nothing reads.
+  auto request_rows = [&](int k, int nb) {
+    for (int b = 0; b < nb; ++b) {
+      const float* src = o_base + (int64_t)(k + b) * o_chunk;
+      for (int q = 0; q < pairs; ++q) {
+        const int r = min(2 * q + (lane >> 5), G - 1);
+        dma16_policy<kLoadLdsDeviceScope>(src + r * kHeadDim + 4 * (lane & 31), scratch + (b * G + 2 * q) * 512);
+      }
+    }
+  };
+  // Log-sum-exps of chunks k0 + lane (clamped: a repeated chunk leaves the
+  // maximum unchanged and gets weight 0 below).
+  auto load_lse = [&](int k0, float (&v)[16]) {
     const float* row = lse_base + min(k0 + lane, nchunks - 1) * lse_chunk;
-    float v[16];
 #pragma unroll
     for (int g = 0; g < 16; ++g)
       if (g < G) v[g] = ld_coherent(row + g);
+  };
+
+  const int nb0 = min(batch, nchunks);
+  request_rows(0, nb0);
+  float v0[16];  // log-sum-exps of chunks 0..63, kept for the weights
+  load_lse(0, v0);
+  float mx[16];
+#pragma unroll
+  for (int g = 0; g < 16; ++g) mx[g] = v0[g];
+  for (int k0 = 64; k0 < nchunks; k0 += 64) {
+    float v[16];
+    load_lse(k0, v);
 #pragma unroll
     for (int g = 0; g < 16; ++g)
       if (g < G) mx[g] = fmaxf(mx[g], v[g]);
@@ -693,23 +729,18 @@ __device__ __attribute__((noinline)) void merge_partials(MergeArgs p, int s, int
       mx[g] = v;
     }
   }
-  // A chunk's G rows are contiguous (G * 512 bytes); `batch` chunks fill at
-  // most 16 rows of scratch.
-  const int batch = max(1, 16 / G);
-  const int64_t o_chunk = (int64_t)Hkv * G * kHeadDim;
-  const float* o_base = p.part_o + ((int64_t)pbase * Hkv + h) * G * kHeadDim;
-  const int pairs = (G + 1) / 2;  // 1 KB copies per chunk (two rows each)
-  const int d = 2 * lane;
   float a0[16], a1[16], wsum[16];
 #pragma unroll
   for (int g = 0; g < 16; ++g) a0[g] = a1[g] = wsum[g] = 0.f;
   for (int k0 = 0; k0 < nchunks; k0 += 64) {
     const int k = k0 + lane;
-    const float* row = lse_base + min(k, nchunks - 1) * lse_chunk;
     float w[16];
+    if (k0 == 0) {
 #pragma unroll
-    for (int g = 0; g < 16; ++g)
-      if (g < G) w[g] = ld_coherent(row + g);
+      for (int g = 0; g < 16; ++g) w[g] = v0[g];
+    } else {
+      load_lse(k0, w);
+    }
 #pragma unroll
     for (int g = 0; g < 16; ++g) {
       if (g < G) {
@@ -720,17 +751,7 @@ __device__ __attribute__((noinline)) void merge_partials(MergeArgs p, int s, int
     const int cnt = min(64, nchunks - k0);
     for (int j0 = 0; j0 < cnt; j0 += batch) {
       const int nb = min(batch, cnt - j0);
-      // Row pair (2q, 2q+1) of chunk j0 + b lands at scratch + (b*G + 2q)*512;
-      // lanes 32..63 of an odd G's last pair re-read row 2q (in bounds) into
-      // the next row slot, which nothing reads.
-      for (int b = 0; b < nb; ++b) {
-        const float* src = o_base + (int64_t)(k0 + j0 + b) * o_chunk;
-        for (int q = 0; q < pairs; ++q) {
-          const int r = min(2 * q + (lane >> 5), G - 1);
-          dma16_policy<kLoadLdsDeviceScope>(src + r * kHeadDim + 4 * (lane & 31),
-                                            scratch + (b * G + 2 * q) * 512);
-        }
-      }
+      if (k0 + j0 > 0) request_rows(k0 + j0, nb);  // the first batch is already in flight
       __builtin_amdgcn_s_waitcnt(kVmcnt0);
       wave_lds_fence();
       for (int b = 0; b < nb; ++b) {

@@ -119,6 +119,29 @@ def test_piece_plans_through_c_abi(gpu, waves, per_wave, min_pages):
     assert int(ws[:8].view(torch.int32).abs().sum().item()) == 0
 
 
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (24, 8), (40, 8), (128, 8)])
+def test_merge_of_one_page_pieces_for_every_group_shape(gpu, hq, hkv):
+    # One-page pieces cut a 2049-token context into 129 chunks: merges with
+    # more than 64 chunks and several staged batches, for G = 1, 3, 5 and 16
+    # (odd G stages one spare row per batch, which must stay inside the
+    # merge scratch).
+    ctx = [2049, 300, 17, 1]
+    batch = make_paged_batch(67, [1] * len(ctx), ctx, 0, hq, hkv)
+    common, q, kc, vc = _to(batch, gpu)
+    counts = np.asarray([(n + 15) // 16 for n in ctx])
+    items, nw, slots = make_decode_plan(counts, 0, 0, hkv, 5000, 64, 1)
+    assert int(items[:, 4].max()) == 129
+    ws = torch.zeros(ops.decode_workspace_bytes(len(ctx), slots, hkv, hq // hkv), dtype=torch.uint8, device=gpu)
+    out = torch.full_like(q, float("nan"))
+    args = (q, kc, vc, common.block_tables, common.seq_lens, _to_device(items, gpu), items.shape[0], nw,
+            len(ctx), slots, out, ws, 128 ** -0.5)
+    ops.paged_decode(*args)
+    first = out.clone()
+    assert_attention_close(first, _expected(batch))
+    ops.paged_decode(*args)
+    assert torch.equal(out, first)
+
+
 def test_stale_nan_rows_past_seq_len_do_not_leak(gpu, monkeypatch):
     monkeypatch.setenv("MVA_DECODE_WAVES", "100000")
     ctx = [5, 16, 33, 300, 129]

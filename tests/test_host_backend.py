@@ -254,5 +254,12 @@ def test_prefill_items_cover_every_tile_once(seed):
     got = sorted((int(s), int(t)) for s, t in items[:, :2])
     want = sorted((s, t) for s in range(q_ub.size) for t in range(0, int(q_ub[s]), tile))
     assert got == want
+    # Grouped by sequence, longest context first; inside a sequence the
+    # tiles with the most keys come first.
+    seqs = [int(s) for s in items[:, 0]]
+    groups = [s for i, s in enumerate(seqs) if i == 0 or s != seqs[i - 1]]
+    assert sorted(groups) == list(range(q_ub.size)), "each sequence's tiles are contiguous"
+    assert all(kv_ub[a] >= kv_ub[b] for a, b in zip(groups, groups[1:])), "longest context first"
     cost = [int(kv_ub[s] - q_ub[s] + min(t + tile, q_ub[s])) for s, t in items[:, :2]]
-    assert all(a >= b for a, b in zip(cost, cost[1:])), "largest key count first"
+    assert all(a >= b for a, b, sa, sb in zip(cost, cost[1:], seqs, seqs[1:]) if sa == sb), \
+        "largest key count first within a sequence"
