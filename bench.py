@@ -125,12 +125,12 @@ def headline(args, device):
     md = plan.metadata
     out = torch.empty_like(q)
     ws = backend._get_workspace(
-        ops.decode_workspace_bytes(common.num_seqs, md.num_decode_part_slots, hkv, hq // hkv), device)
+        ops.decode_workspace_bytes(md.num_decode_part_slots, hkv, hq // hkv), device)
 
     def decode_only(i):
         kc, vc = caches[i % copies]
         ops.paged_decode(q, kc, vc, md.block_tables, md.seq_lens, md.decode_items, md.num_decode_items,
-                         md.num_decode_waves, common.num_seqs,
+                         md.num_decode_waves, md.decode_merges, md.num_decode_merges,
                          md.num_decode_part_slots, out, ws, backend.softmax_scale)
 
     ms_decode = time_launches(decode_only, max(args.steps, 200), args.warmup)
@@ -304,12 +304,12 @@ def run_only(args, device):
         md = backend.build_plan(common).metadata
         out = torch.empty_like(q)
         ws = backend._get_workspace(
-            ops.decode_workspace_bytes(common.num_seqs, md.num_decode_part_slots, hkv, hq // hkv), device)
+            ops.decode_workspace_bytes(md.num_decode_part_slots, hkv, hq // hkv), device)
         for i in range(n):
             kc, vc = caches[i % copies]
             ops.paged_decode(q, kc, vc, md.block_tables, md.seq_lens, md.decode_items, md.num_decode_items,
-                             md.num_decode_waves, common.num_seqs, md.num_decode_part_slots, out, ws,
-                             backend.softmax_scale)
+                             md.num_decode_waves, md.decode_merges, md.num_decode_merges,
+                             md.num_decode_part_slots, out, ws, backend.softmax_scale)
         torch.cuda.synchronize()
         print(json.dumps({"only": args.only, "bytes_per_launch": decode_bytes(batch, hq, hkv), "launches": n,
                           "waves": md.num_decode_waves, "pieces": md.num_decode_items}))

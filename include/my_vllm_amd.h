@@ -60,14 +60,14 @@ int mva_kv_store(const void* key, int64_t key_row_stride, const void* value,
                  int dtype, void* stream);
 
 /*
- * Bytes of device workspace mva_paged_decode needs for `num_seqs` sequences
- * and `num_part_slots` split-K partial slots (a 256-byte scheduler area,
- * per-(sequence, KV head) arrival counters, partial outputs).  The workspace
- * must be zeroed once when first allocated; the kernels leave its counters
- * zeroed again on return.  Launches that share a workspace must not overlap.
+ * Bytes of device workspace mva_paged_decode / mva_paged_mixed need for
+ * `num_part_slots` split-K partial slots (a scheduler area of piece-claim
+ * counters, then fp32 partial outputs and log-sum-exps), or -1 for invalid
+ * arguments.  The workspace must be zeroed once when first allocated; the
+ * kernels leave the counters zeroed again on return.  Launches that share a
+ * workspace must not overlap.
  */
-int64_t mva_decode_workspace_bytes(int64_t num_seqs, int64_t num_part_slots, int num_kv_heads,
-                                   int group);
+int64_t mva_decode_workspace_bytes(int64_t num_part_slots, int num_kv_heads, int group);
 
 /*
  * Paged GQA decode (one query token per sequence) over an NHD page cache
@@ -82,14 +82,18 @@ int64_t mva_decode_workspace_bytes(int64_t num_seqs, int64_t num_part_slots, int
  *         (at most 128 pages), piece `chunk` of `n_chunks`; split-K partial
  *         slots part_base .. part_base + n_chunks - 1 (unused when
  *         n_chunks == 1); output row q_row.
- *   num_waves (1 .. num_items): wavefronts launched; wavefront w starts on
- *         piece w and then claims pieces num_waves, num_waves + 1, ... from a
- *         counter in the workspace, so pieces should be listed longest first.
+ *   num_waves (1 .. num_items): wavefronts launched; wavefront w runs
+ *         pieces w and num_waves + w and then claims later pieces from
+ *         counters in the workspace, so pieces should be listed longest first.
+ *   merges [num_merges, 8] int32: one piece descriptor (chunk 0) of every
+ *         (sequence, KV head) cut into n_chunks > 1 pieces; a second kernel on
+ *         `stream` combines each one's partials into its output rows.
+ *   num_part_slots: split-K partial slots the pieces use (part_base + chunk <
+ *         num_part_slots); sizes the workspace.
  *   out:  out + row*out_token_stride + head*out_head_stride, `dtype`.
  * softmax over keys j < seq_len with scale `softmax_scale`; fp32 accumulate.
- * The pieces of one (sequence, KV head) are merged in the same launch by the
- * last one to finish.  Requires head_dim 128, page_size 16, num_q_heads /
- * num_kv_heads <= 16, 16-byte aligned q/cache buffers and strides.
+ * Requires head_dim 128, page_size 16, num_q_heads / num_kv_heads <= 16,
+ * 16-byte aligned q/cache buffers and strides.
  * Replaces FlashInfer BatchDecodeWithPagedKVCacheWrapper.plan/run as used by
  * the reference's DECODE route (nanovllm/layers/attention_backend.py:826-840,
  * :995-997) and the decode half of MIXED_SPLIT (:874-889, :1020-1025).
@@ -98,8 +102,8 @@ int mva_paged_decode(const void* q, int64_t q_token_stride, int64_t q_head_strid
                      const void* k_cache, const void* v_cache, int64_t num_pages,
                      int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
                      int64_t block_table_stride, const int32_t* seq_lens, const int32_t* items,
-                     int64_t num_items, int64_t num_waves, int64_t num_seqs,
-                     int64_t num_part_slots, void* out,
+                     int64_t num_items, int64_t num_waves, const int32_t* merges,
+                     int64_t num_merges, int64_t num_part_slots, void* out,
                      int64_t out_token_stride, int64_t out_head_stride, void* workspace,
                      int64_t workspace_bytes, int num_q_heads, int num_kv_heads, int head_dim,
                      int page_size, float softmax_scale, int dtype, void* stream);
@@ -144,8 +148,8 @@ int mva_paged_mixed(const void* q, int64_t q_token_stride, int64_t q_head_stride
                     int64_t block_table_stride, const int32_t* seq_lens,
                     const int32_t* query_start_loc, const int32_t* prefill_items,
                     int64_t num_prefill_items, const int32_t* decode_items,
-                    int64_t num_decode_items, int64_t num_decode_waves, int64_t num_seqs,
-                    int64_t num_part_slots,
+                    int64_t num_decode_items, int64_t num_decode_waves,
+                    const int32_t* decode_merges, int64_t num_decode_merges, int64_t num_part_slots,
                     void* out, int64_t out_token_stride, int64_t out_head_stride,
                     void* workspace, int64_t workspace_bytes, int num_q_heads, int num_kv_heads,
                     int head_dim, int page_size, float softmax_scale, int dtype, void* stream);

@@ -32,14 +32,15 @@ _SIGNATURES = {
         _i32,
         [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _i32, _i64, _i64, _i32, _c_void_p],
     ),
-    "mva_decode_workspace_bytes": (_i64, [_i64, _i64, _i32, _i32]),
+    "mva_decode_workspace_bytes": (_i64, [_i64, _i32, _i32]),
     "mva_paged_decode": (
         _i32,
         [
             _c_void_p, _i64, _i64,  # q, q_token_stride, q_head_stride
             _c_void_p, _c_void_p, _i64, _i64, _i64,  # k_cache, v_cache, num_pages, page_stride, token_stride
             _c_void_p, _i64, _c_void_p,  # block_tables, block_table_stride, seq_lens
-            _c_void_p, _i64, _i64, _i64, _i64,  # items, num_items, num_waves, num_seqs, slots
+            _c_void_p, _i64, _i64,  # items, num_items, num_waves
+            _c_void_p, _i64, _i64,  # merges, num_merges, num_part_slots
             _c_void_p, _i64, _i64,  # out, out_token_stride, out_head_stride
             _c_void_p, _i64,  # workspace, workspace_bytes
             _i32, _i32, _i32, _i32, _f32, _i32, _c_void_p,  # heads, head_dim, page, scale, dtype, stream
@@ -63,7 +64,8 @@ _SIGNATURES = {
             _c_void_p, _i64, _i64,
             _c_void_p, _c_void_p, _i64, _i64, _i64,
             _c_void_p, _i64, _c_void_p, _c_void_p,
-            _c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _i64,  # prefill, decode items, waves, seqs, slots
+            _c_void_p, _i64, _c_void_p, _i64, _i64,  # prefill items, decode items, waves
+            _c_void_p, _i64, _i64,  # decode merges, num merges, num_part_slots
             _c_void_p, _i64, _i64,
             _c_void_p, _i64,
             _i32, _i32, _i32, _i32, _f32, _i32, _c_void_p,

@@ -269,7 +269,8 @@ class MI355XAttentionMetadata:
 
     ``decode_items`` is int32 ``[num_decode_items, 8]`` pieces, claimed by
     ``num_decode_waves`` wavefronts (see ``make_decode_plan``); ``None``
-    without decode sequences.
+    without decode sequences.  ``decode_merges`` lists the split segments
+    (``ops.decode_merge_list``) whose partials the merge kernel combines.
     ``prefill_items`` is int32 ``[num_prefill_items, 4]`` query tiles (see
     ``make_prefill_items``).  ``kv_indptr`` is the page CSR offset list (host
     ints): sequence ``s`` owns pages ``block_tables[s, :kv_indptr[s+1]-kv_indptr[s]]``.
@@ -285,6 +286,8 @@ class MI355XAttentionMetadata:
     num_decode_items: int = 0
     num_decode_waves: int = 0
     num_decode_part_slots: int = 0
+    decode_merges: torch.Tensor | None = None
+    num_decode_merges: int = 0
     prefill_items: torch.Tensor | None = None
     num_prefill_items: int = 0
 
@@ -559,7 +562,9 @@ class MI355XAttentionBackendMixin:
                 raise ValueError("trusted num_prefill_kv_blocks must match block_counts")
 
         decode_items = None
+        decode_merges = None
         num_decode_items = 0
+        num_decode_merges = 0
         num_decode_waves = 0
         num_part_slots = 0
         if common.num_decode_seqs:
@@ -575,8 +580,13 @@ class MI355XAttentionBackendMixin:
                 self.num_kv_heads,
                 waves,
             )
+            merges = ops.decode_merge_list(items)
             num_decode_items = items.shape[0]
-            decode_items = _to_device(items, block_tables.device)
+            num_decode_merges = merges.shape[0]
+            # Pieces and merge entries share one host-to-device copy.
+            both = _to_device(np.concatenate([items, merges]), block_tables.device)
+            decode_items = both[:num_decode_items]
+            decode_merges = both[num_decode_items:]
         prefill_items = None
         num_prefill_items = 0
         if common.num_prefill_seqs:
@@ -608,6 +618,8 @@ class MI355XAttentionBackendMixin:
             num_decode_items=num_decode_items,
             num_decode_waves=num_decode_waves,
             num_decode_part_slots=num_part_slots,
+            decode_merges=decode_merges,
+            num_decode_merges=num_decode_merges,
             prefill_items=prefill_items,
             num_prefill_items=num_prefill_items,
         )
@@ -736,9 +748,7 @@ class MI355XAttentionBackendMixin:
 
     def _run_decode(self, q, k_cache, v_cache, common, metadata: MI355XAttentionMetadata, output) -> None:
         group = self.num_q_heads // self.num_kv_heads
-        ws_bytes = ops.decode_workspace_bytes(
-            common.num_seqs, metadata.num_decode_part_slots, self.num_kv_heads, group
-        )
+        ws_bytes = ops.decode_workspace_bytes(metadata.num_decode_part_slots, self.num_kv_heads, group)
         workspace = self._get_workspace(ws_bytes, q.device)
         ops.paged_decode(
             q,
@@ -749,7 +759,8 @@ class MI355XAttentionBackendMixin:
             metadata.decode_items,
             metadata.num_decode_items,
             metadata.num_decode_waves,
-            common.num_seqs,
+            metadata.decode_merges,
+            metadata.num_decode_merges,
             metadata.num_decode_part_slots,
             output,
             workspace,
@@ -772,9 +783,7 @@ class MI355XAttentionBackendMixin:
 
     def _run_mixed(self, q, k_cache, v_cache, common, metadata: MI355XAttentionMetadata, output) -> None:
         group = self.num_q_heads // self.num_kv_heads
-        ws_bytes = ops.decode_workspace_bytes(
-            common.num_seqs, metadata.num_decode_part_slots, self.num_kv_heads, group
-        )
+        ws_bytes = ops.decode_workspace_bytes(metadata.num_decode_part_slots, self.num_kv_heads, group)
         workspace = self._get_workspace(ws_bytes, q.device)
         ops.paged_mixed(
             q,
@@ -788,7 +797,8 @@ class MI355XAttentionBackendMixin:
             metadata.decode_items,
             metadata.num_decode_items,
             metadata.num_decode_waves,
-            common.num_seqs,
+            metadata.decode_merges,
+            metadata.num_decode_merges,
             metadata.num_decode_part_slots,
             output,
             workspace,

@@ -35,10 +35,9 @@
 //    storage type for the PV MFMA; the O rescale is skipped unless the
 //    running max grows by more than 8 (log2 units).
 //  * A (sequence, KV head) split into several pieces (split-K) gets one fp32
-//    partial per piece (o / l, log2-sum-exp); the last piece to finish,
-//    detected with a device-scope counter, merges the partials, so one launch
-//    produces the final output.  Counters are reset by the merger, so the
-//    workspace only has to be zeroed when first allocated.
+//    partial per piece (o / l, log2-sum-exp); a second, small kernel on the
+//    same stream merges the partials of every split (sequence, KV head), one
+//    wavefront per query head, so the page stream never waits on a merge.
 #pragma once
 
 #include "mva_common.h"
@@ -81,7 +80,6 @@ struct DecodeParams {
   void* out;
   int64_t out_tok_stride;
   int64_t out_head_stride;
-  int32_t* counters;  // [num_seqs][Hkv]
   float* part_lse;    // [slots][Hkv][G]
   float* part_o;      // [slots][Hkv][G][D]
   int num_kv_heads;
@@ -97,29 +95,6 @@ __device__ inline float wave_sum16(float x) {
   x += __shfl_xor(x, 16);
   return x + __shfl_xor(x, 32);
 }
-
-// Everything a split-K merge needs, passed by value: the merge is an
-// out-of-line call, so its registers do not add to the page loop's.
-// Partial rows (512 bytes each) the merge stages in LDS at once: one page
-// buffer inside the page loop (the other may hold an in-flight DMA), both at
-// the wavefront's exit.
-constexpr int kMergeRowsInLoop = 2 * kDecodePageBytes / 512;
-constexpr int kMergeRowsAtExit = 4 * kDecodePageBytes / 512;
-
-struct MergeArgs {
-  float* part_lse;
-  float* part_o;
-  int32_t* counters;
-  void* out;
-  int64_t out_tok_stride;
-  int64_t out_head_stride;
-  int num_kv_heads;
-  int group;
-};
-
-template <typename T>
-__device__ __attribute__((noinline)) void merge_partials(MergeArgs a, int s, int h, int pbase, int nchunks,
-                                                         int64_t qrow, lds_u8* scratch, int scratch_rows);
 
 // Scalar (SMEM) loads of data that is read-only for the whole launch (work
 // lists, page tables, lengths).  The constant address space tells the
@@ -147,7 +122,6 @@ __device__ inline int sload(const int32_t* base, int64_t idx) { return ((const_i
 // Per-iteration memory work of a decode wavefront, issued as one asm
 // statement, in this order:
 //   * lane 0: claim = atomic_add(claim_ptr, 1) if `claiming`;
-//   * lane 0: arrival = atomic_add(arrive_ptr, 1) if `arriving`;
 //   * all lanes, if `claiming`: the next piece's page-table words
 //     (bt0 -> bt_lo, bt1 -> bt_hi) and query fragments (q .. q + 63 -> qv);
 //   * if kDma: the 8 DMAs of one page of one KV head (4 to lds_v, 4 to
@@ -159,24 +133,21 @@ __device__ inline int sload(const int32_t* base, int64_t idx) { return ((const_i
 // so DMA i holds d-chunks 4i..4i+3 of all 16 tokens.  The K A-operand read
 // (16 tokens at one chunk) and the V transposed read (4 tokens x 2 chunks
 // per 16-lane group) both cover whole 256-byte bank rows.
-// `claiming` and `arriving` are wave-uniform.  Outputs not issued keep their
-// previous contents (claim/arrival: unspecified).
+// `claiming` is wave-uniform.  Outputs not issued keep their previous
+// contents (claim: unspecified).
 struct DecodeStepIo {
   int claim;
-  int arrival;
   int bt_lo;
   int bt_hi;
   u32x4 qv[4];
 };
 
 template <bool kDma>
-__device__ inline void decode_step(DecodeStepIo& io, int claiming, int arriving, int* claim_ptr, int* arrive_ptr,
-                                   const int32_t* bt0, const int32_t* bt1, const void* q, const void* v_src,
+__device__ inline void decode_step(DecodeStepIo& io, int claiming, int* claim_ptr, const int32_t* bt0, const int32_t* bt1, const void* q, const void* v_src,
                                    const void* k_src, uint32_t lds_v, uint32_t lds_k) {
   uint64_t saved;
   uint32_t m0_saved;
   const int on_c = __builtin_amdgcn_readfirstlane(claiming != 0 ? 1 : 0);
-  const int on_a = __builtin_amdgcn_readfirstlane(arriving != 0 ? 1 : 0);
   lds_v = __builtin_amdgcn_readfirstlane(lds_v);
   lds_k = __builtin_amdgcn_readfirstlane(lds_k);
   const char* v = (const char*)v_src;
@@ -187,8 +158,6 @@ __device__ inline void decode_step(DecodeStepIo& io, int claiming, int arriving,
         "s_mov_b32 exec_lo, %[onc]\n\t"
         "s_mov_b32 exec_hi, 0\n\t"
         "global_atomic_add %[cl], %[cp], %[one], off sc0\n\t"
-        "s_mov_b32 exec_lo, %[ona]\n\t"
-        "global_atomic_add %[ar], %[ap], %[one], off sc0\n\t"
         "s_cmp_eq_u32 %[onc], 0\n\t"
         "s_cselect_b64 exec, 0, %[sv]\n\t"
         "global_load_dword %[blo], %[b0], off\n\t"
@@ -225,10 +194,10 @@ __device__ inline void decode_step(DecodeStepIo& io, int claiming, int arriving,
         "global_load_lds_dwordx4 %[k3], off\n\t"
         "s_mov_b32 m0, %[m0s]\n\t"
         "s_waitcnt vmcnt(8)"
-        : [cl] "=&v"(io.claim), [ar] "=&v"(io.arrival), [blo] "+v"(io.bt_lo), [bhi] "+v"(io.bt_hi),
+        : [cl] "=&v"(io.claim), [blo] "+v"(io.bt_lo), [bhi] "+v"(io.bt_hi),
           [q0] "+v"(io.qv[0]), [q1] "+v"(io.qv[1]), [q2] "+v"(io.qv[2]), [q3] "+v"(io.qv[3]), [sv] "=&s"(saved),
           [m0s] "=&s"(m0_saved)
-        : [onc] "s"(on_c), [ona] "s"(on_a), [cp] "v"(claim_ptr), [ap] "v"(arrive_ptr), [one] "v"(1),
+        : [onc] "s"(on_c), [cp] "v"(claim_ptr), [one] "v"(1),
           [b0] "v"(bt0), [b1] "v"(bt1), [qp] "v"(q), [lv] "s"(lds_v), [lk] "s"(lds_k), [v0] "v"(v),
           [v1] "v"(v + 64), [v2] "v"(v + 128), [v3] "v"(v + 192), [k0] "v"(k), [k1] "v"(k + 64),
           [k2] "v"(k + 128), [k3] "v"(k + 192)
@@ -239,8 +208,6 @@ __device__ inline void decode_step(DecodeStepIo& io, int claiming, int arriving,
         "s_mov_b32 exec_lo, %[onc]\n\t"
         "s_mov_b32 exec_hi, 0\n\t"
         "global_atomic_add %[cl], %[cp], %[one], off sc0\n\t"
-        "s_mov_b32 exec_lo, %[ona]\n\t"
-        "global_atomic_add %[ar], %[ap], %[one], off sc0\n\t"
         "s_cmp_eq_u32 %[onc], 0\n\t"
         "s_cselect_b64 exec, 0, %[sv]\n\t"
         "global_load_dword %[blo], %[b0], off\n\t"
@@ -251,9 +218,9 @@ __device__ inline void decode_step(DecodeStepIo& io, int claiming, int arriving,
         "global_load_dwordx4 %[q3], %[qp], off offset:48\n\t"
         "s_mov_b64 exec, %[sv]\n\t"
         "s_waitcnt vmcnt(0)"
-        : [cl] "=&v"(io.claim), [ar] "=&v"(io.arrival), [blo] "+v"(io.bt_lo), [bhi] "+v"(io.bt_hi),
+        : [cl] "=&v"(io.claim), [blo] "+v"(io.bt_lo), [bhi] "+v"(io.bt_hi),
           [q0] "+v"(io.qv[0]), [q1] "+v"(io.qv[1]), [q2] "+v"(io.qv[2]), [q3] "+v"(io.qv[3]), [sv] "=&s"(saved)
-        : [onc] "s"(on_c), [ona] "s"(on_a), [cp] "v"(claim_ptr), [ap] "v"(arrive_ptr), [one] "v"(1),
+        : [onc] "s"(on_c), [cp] "v"(claim_ptr), [one] "v"(1),
           [b0] "v"(bt0), [b1] "v"(bt1), [qp] "v"(q)
         : "memory", "scc");
   }
@@ -282,8 +249,10 @@ static_assert((kDecodeClaimCounters + 1) * kDecodeSchedLineInts * 4 <= kDecodeSc
 // kDecodeWaveLdsBytes of LDS.
 //
 // Piece order: wavefront w takes piece w, then piece W + w (W = num_waves),
-// then pieces 2W + C*k + (w mod C) for k drawn from claim counter (w mod C),
-// C = min(32, W).  Three pieces are tracked: X (being computed), Y (its
+// then pieces 2W + C*k + j for k drawn from claim counter j = (w / 8) mod C,
+// C = min(32, max(1, W / 8)).  Blocks are dealt to the 8 XCDs round-robin,
+// so wavefronts of every XCD share each counter and no counter's share of
+// the queue waits on one slower XCD.  Three pieces are tracked: X (being computed), Y (its
 // successor: descriptor and length known, page table and queries loaded
 // during X's first page) and Z (Y's successor, claimed at X's first page;
 // its descriptor is fetched right after that page).  The page stream runs
@@ -293,11 +262,8 @@ static_assert((kDecodeClaimCounters + 1) * kDecodeSchedLineInts * 4 <= kDecodeSc
 // page-table registers (readlane); the loop issues no memory access per
 // page other than the page itself.
 //
-// Split-K arrivals: a split piece stores its partial when it ends (iteration
-// k); the stores are complete after the wait of iteration k+1, so the
-// arrival counter is incremented at the top of iteration k+2 and examined
-// after that iteration's wait.  The last arrival merges, in the same
-// iteration, after the page is computed (that page buffer is then free).
+// A split piece stores its partial when it ends; decode_merge_wave combines
+// the partials in the kernel that follows on the same stream.
 template <typename T>
 __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
   typedef typename Elem<T>::v8 V8;
@@ -309,10 +275,10 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
   const int Hkv = p.num_kv_heads;
   const int W = p.num_waves;
   const int N = p.num_items;
-  const int C = min(kDecodeClaimCounters, W);
+  const int C = min(kDecodeClaimCounters, max(1, W >> 3));
+  const int jc = (wave >> 3) % C;
   const bool q_lane = c < G;
-  int* const claim_ctr = p.sched + (wave % C) * kDecodeSchedLineInts;
-  const MergeArgs margs{p.part_lse, p.part_o, p.counters, p.out, p.out_tok_stride, p.out_head_stride, Hkv, G};
+  int* const claim_ctr = p.sched + jc * kDecodeSchedLineInts;
 
   // Descriptor fields: {seq, page_begin, page_end, chunk, n_chunks, part_base, q_row, kv_head}.
   auto desc_at = [&](int idx) -> i32x8 { return ((const_i32x8*)p.items)[idx]; };
@@ -360,11 +326,6 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) io.qv[j] = u32x4{0u, 0u, 0u, 0u};
 
-  // Split-K pieces whose partial stores are in flight (arrival counter
-  // offset and piece index; index -1: none): `a` was stored two iterations
-  // back (its arrival is due at the next loop top), `b` in the previous one.
-  int a_ctr = 0, a_idx = -1, a_n = 0, b_ctr = 0, b_idx = -1, b_n = 0;
-  int xi = wave;
 
   f32x4 o[8];  // o[mt][r] = O^T[d = 16*mt + 4*q4 + r][g = c]
 #pragma unroll
@@ -468,7 +429,7 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
     const int64_t base = (int64_t)page_of(bt_lo, bt_hi, 0) * p.page_stride + X[7] * kHeadDim;
     const int64_t lane_off = (lane & 15) * p.tok_stride + 8 * (lane >> 4);
     const uint32_t lds_k = (uint32_t)(uintptr_t)lds;
-    decode_step<true>(io, 0, 0, claim_ctr, p.counters, bt_word(X, lane), bt_word(X, 64 + lane), q_addr(X),
+    decode_step<true>(io, 0, claim_ctr, bt_word(X, lane), bt_word(X, 64 + lane), q_addr(X),
                       (const T*)p.v_cache + base + lane_off, (const T*)p.k_cache + base + lane_off,
                       lds_k + kDecodePageBytes, lds_k);
   }
@@ -498,15 +459,8 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
     fh = __builtin_amdgcn_readfirstlane(fh);
     fpg = __builtin_amdgcn_readfirstlane(fpg);
     fvalid = __builtin_amdgcn_readfirstlane(fvalid);
-    xi = __builtin_amdgcn_readfirstlane(xi);
     yi = __builtin_amdgcn_readfirstlane(yi);
     zi = __builtin_amdgcn_readfirstlane(zi);
-    a_ctr = __builtin_amdgcn_readfirstlane(a_ctr);
-    a_idx = __builtin_amdgcn_readfirstlane(a_idx);
-    a_n = __builtin_amdgcn_readfirstlane(a_n);
-    b_ctr = __builtin_amdgcn_readfirstlane(b_ctr);
-    b_idx = __builtin_amdgcn_readfirstlane(b_idx);
-    b_n = __builtin_amdgcn_readfirstlane(b_n);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       X[k] = __builtin_amdgcn_readfirstlane(X[k]);
@@ -517,35 +471,26 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
     lds_u8* nxt = lds + (buf ^ 1) * (2 * kDecodePageBytes);
 
     // One asm statement issues Y's page table and queries and the claim for
-    // Z (first page of X), the arrival of the split piece whose stores the
-    // previous wait completed, and the next page's DMAs, then waits for all
-    // of it but those DMAs (see decode_step).
+    // Z (first page of X) and the next page's DMAs, then waits for all of it
+    // but those DMAs (see decode_step).
     const int claiming = (i == 0 && yi < N) ? 1 : 0;
-    const int arriving = a_idx >= 0 ? 1 : 0;
-    const int d_idx = a_idx;
-    const int d_n = a_n;
     if (fvalid) {
       const int64_t base = (int64_t)fpg * p.page_stride + fh * kHeadDim;
       const int64_t lane_off = (lane & 15) * p.tok_stride + 8 * (lane >> 4);
       const uint32_t lds_k = (uint32_t)(uintptr_t)nxt;
-      decode_step<true>(io, claiming, arriving, claim_ctr, p.counters + a_ctr, bt_word(Y, lane), bt_word(Y, 64 + lane),
+      decode_step<true>(io, claiming, claim_ctr, bt_word(Y, lane), bt_word(Y, 64 + lane),
                         q_addr(Y), (const T*)p.v_cache + base + lane_off, (const T*)p.k_cache + base + lane_off,
                         lds_k + kDecodePageBytes, lds_k);
     } else {
-      decode_step<false>(io, claiming, arriving, claim_ctr, p.counters + a_ctr, bt_word(Y, lane),
-                         bt_word(Y, 64 + lane), q_addr(Y), nullptr, nullptr, 0, 0);
+      decode_step<false>(io, claiming, claim_ctr, bt_word(Y, lane), bt_word(Y, 64 + lane), q_addr(Y), nullptr,
+                         nullptr, 0, 0);
     }
     wave_lds_fence();
-    a_ctr = b_ctr;
-    a_idx = b_idx;
-    a_n = b_n;
-    b_idx = -1;
     const int craw = io.claim;
-    const int araw = io.arrival;
     const int nbt_lo = io.bt_lo;
     const int nbt_hi = io.bt_hi;
 
-    if (claiming) zi = 2 * W + C * __builtin_amdgcn_readfirstlane(craw) + wave % C;
+    if (claiming) zi = 2 * W + C * __builtin_amdgcn_readfirstlane(craw) + jc;
     // Z's descriptor is needed now only when this is X's last page and Y is
     // a single page (Z's first page is then the next DMA); otherwise it is
     // fetched after the compute below.
@@ -554,7 +499,6 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
       Z = desc_at(zi);
       z_len = sload(p.seq_lens, Z[0]);
     }
-    const bool merging = arriving && __builtin_amdgcn_readfirstlane(araw) == d_n - 1;
 
     // The page after the one just issued (for X's last page: Y's second,
     // or Z's first when Y is a single page).
@@ -589,22 +533,12 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
       Z = desc_at(zi);
       z_len = sload(p.seq_lens, Z[0]);
     }
-    if (merging) {
-      const i32x8 D = desc_at(d_idx);
-      merge_partials<T>(margs, D[0], D[7], D[5], D[4], D[6], cur, kMergeRowsInLoop);
-    }
     buf ^= 1;
     if (++i < np) continue;
 
     // ---- piece boundary ----
     finish_piece();
-    if (X[4] > 1) {
-      b_ctr = X[0] * Hkv + X[7];
-      b_idx = xi;
-      b_n = X[4];
-    }
     if (yi >= N) break;
-    xi = yi;
     X = Y;
     seq_len = y_len;
     bt_lo = io.bt_lo;
@@ -623,23 +557,11 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
     i = 0;
   }
 
-  // Settle the split pieces whose arrivals are still pending (their stores
-  // are complete after the drain), then count this wavefront out; the last
-  // one resets the scheduler for the next launch.  Every claim this
-  // wavefront made has returned by now, so all claims precede the reset.
+  // Count this wavefront out; the last one resets the scheduler for the next
+  // launch.  Every claim this wavefront made has returned by now (each was
+  // retired by the wait of the iteration that issued it), so all claims
+  // precede the reset.
   __builtin_amdgcn_s_waitcnt(kVmcnt0);
-#pragma nounroll
-  for (int k = 0; k < 2; ++k) {
-    const int idx = k == 0 ? a_idx : b_idx;
-    const int ctr = k == 0 ? a_ctr : b_ctr;
-    if (idx >= 0) {
-      const i32x8 D = desc_at(idx);
-      int prev = 0;
-      if (lane == 0) prev = __hip_atomic_fetch_add(p.counters + ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (__builtin_amdgcn_readfirstlane(prev) == D[4] - 1)
-        merge_partials<T>(margs, D[0], D[7], D[5], D[4], D[6], lds, kMergeRowsAtExit);
-    }
-  }
   if (lane == 0) {
     int* const exit_ctr = p.sched + kDecodeClaimCounters * kDecodeSchedLineInts;
     const int gone = __hip_atomic_fetch_add(exit_ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -651,140 +573,55 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
   }
 }
 
-// Device-scope (coherent) load of a split-K log-sum-exp written by another CU.
-__device__ inline float ld_coherent(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Cache-policy bits of a device-scope (sc1) global_load_lds.
-constexpr int kLoadLdsDeviceScope = 16;
-
-// Merges the n_chunks split-K partials of (sequence s, KV head h) into the
-// output rows of its G query heads:
-//   o = sum_k w_k o_k / sum_k w_k,  w_k = 2^(lse_k - max_k lse_k).
-// Lane L owns chunks L, L+64, ... in the log-sum-exp pass and output columns
-// d = 2L, 2L+1 in the weighted sum.  The partial rows of up to scratch_rows /
-// G chunks at a time are copied into `scratch` with coherent global_load_lds
-// and summed from there, without holding the rows in registers.  The first
-// batch of rows is requested together with the log-sum-exps, so a merge of
-// up to scratch_rows / G chunks costs one memory round trip.  Resets the
-// arrival counter for the next launch.
+// Split-K merge of one (split segment, query head g): the wavefront's index
+// v selects merge entry v / G (a piece descriptor {seq, -, -, -, n_chunks,
+// part_base, q_row, kv_head} of a segment cut into n_chunks > 1 pieces) and
+// g = v % G, and writes
+//   o = sum_k w_k o_k / sum_k w_k,  w_k = 2^(lse_k - max_k lse_k)
+// over the segment's chunks k.  Lane L owns chunks L, L+64, ... of the
+// log-sum-exp pass and output columns d = 2L, 2L+1 of the weighted sum.
+// Runs in the kernel after the decode kernel, which makes every partial
+// visible.
 template <typename T>
-__device__ __attribute__((noinline)) void merge_partials(MergeArgs p, int s, int h, int pbase, int nchunks,
-                                                         int64_t qrow, lds_u8* scratch, int scratch_rows) {
+__device__ void decode_merge_wave(const DecodeParams& p, const int32_t* __restrict__ merges, int64_t v) {
   const int lane = threadIdx.x & 63;
   const int G = p.group;
   const int Hkv = p.num_kv_heads;
-  const float* lse_base = p.part_lse + ((int64_t)pbase * Hkv + h) * G;  // chunk k: + k*Hkv*G
-  const int64_t lse_chunk = (int64_t)Hkv * G;
-  // A chunk's G rows are contiguous (G * 512 bytes); `batch` chunks fill at
-  // most scratch_rows rows of scratch, counting the spare row an odd G's last
-  // row pair writes.
-  const int batch = max(1, (scratch_rows - (G & 1)) / G);
-  const int64_t o_chunk = (int64_t)Hkv * G * kHeadDim;
-  const float* o_base = p.part_o + ((int64_t)pbase * Hkv + h) * G * kHeadDim;
-  const int pairs = (G + 1) / 2;  // 1 KB copies per chunk (two rows each)
-  const int d = 2 * lane;
-  // Row pair (2q, 2q+1) of chunk k + b lands at scratch + (b*G + 2q)*512;
-  // lanes 32..63 of an odd G's last pair re-read row 2q (in bounds) into the
-  // next row slot, which nothing reads.
-  auto request_rows = [&](int k, int nb) {
-    for (int b = 0; b < nb; ++b) {
-      const float* src = o_base + (int64_t)(k + b) * o_chunk;
-      for (int q = 0; q < pairs; ++q) {
-        const int r = min(2 * q + (lane >> 5), G - 1);
-        dma16_policy<kLoadLdsDeviceScope>(src + r * kHeadDim + 4 * (lane & 31), scratch + (b * G + 2 * q) * 512);
-      }
-    }
-  };
-  // Log-sum-exps of chunks k0 + lane (clamped: a repeated chunk leaves the
-  // maximum unchanged and gets weight 0 below).
-  auto load_lse = [&](int k0, float (&v)[16]) {
-    const float* row = lse_base + min(k0 + lane, nchunks - 1) * lse_chunk;
+  const int32_t* d = merges + (v / G) * kDecodeItemInts;
+  const int g = (int)(v % G);
+  const int n = d[4];
+  const int pbase = d[5];
+  const int64_t qrow = d[6];
+  const int h = d[7];
+  // Partial slot of chunk k (lse index; o row = slot * D).
+  auto slot = [&](int k) -> int64_t { return ((int64_t)(pbase + k) * Hkv + h) * G + g; };
+  float lse0 = lane < n ? p.part_lse[slot(lane)] : -INFINITY;  // chunks 0..63, kept for the weights
+  float mx = lse0;
+  for (int k0 = 64; k0 < n; k0 += 64)
+    if (k0 + lane < n) mx = fmaxf(mx, p.part_lse[slot(k0 + lane)]);
 #pragma unroll
-    for (int g = 0; g < 16; ++g)
-      if (g < G) v[g] = ld_coherent(row + g);
-  };
-
-  const int nb0 = min(batch, nchunks);
-  request_rows(0, nb0);
-  float v0[16];  // log-sum-exps of chunks 0..63, kept for the weights
-  load_lse(0, v0);
-  float mx[16];
-#pragma unroll
-  for (int g = 0; g < 16; ++g) mx[g] = v0[g];
-  for (int k0 = 64; k0 < nchunks; k0 += 64) {
-    float v[16];
-    load_lse(k0, v);
-#pragma unroll
-    for (int g = 0; g < 16; ++g)
-      if (g < G) mx[g] = fmaxf(mx[g], v[g]);
-  }
-#pragma unroll
-  for (int g = 0; g < 16; ++g) {
-    if (g < G) {
-      float v = mx[g];
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-      mx[g] = v;
-    }
-  }
-  float a0[16], a1[16], wsum[16];
-#pragma unroll
-  for (int g = 0; g < 16; ++g) a0[g] = a1[g] = wsum[g] = 0.f;
-  for (int k0 = 0; k0 < nchunks; k0 += 64) {
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  float a0 = 0.f, a1 = 0.f, wsum = 0.f;
+  for (int k0 = 0; k0 < n; k0 += 64) {
     const int k = k0 + lane;
-    float w[16];
-    if (k0 == 0) {
-#pragma unroll
-      for (int g = 0; g < 16; ++g) w[g] = v0[g];
-    } else {
-      load_lse(k0, w);
-    }
-#pragma unroll
-    for (int g = 0; g < 16; ++g) {
-      if (g < G) {
-        w[g] = (k < nchunks && mx[g] != -INFINITY) ? fast_exp2(w[g] - mx[g]) : 0.f;
-        wsum[g] += w[g];
-      }
-    }
-    const int cnt = min(64, nchunks - k0);
-    for (int j0 = 0; j0 < cnt; j0 += batch) {
-      const int nb = min(batch, cnt - j0);
-      if (k0 + j0 > 0) request_rows(k0 + j0, nb);  // the first batch is already in flight
-      __builtin_amdgcn_s_waitcnt(kVmcnt0);
-      wave_lds_fence();
-      for (int b = 0; b < nb; ++b) {
-#pragma unroll
-        for (int g = 0; g < 16; ++g) {
-          if (g < G) {
-            const float wb = __builtin_bit_cast(
-                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w[g]), j0 + b));
-            const f32x2 v = lds_ld8<f32x2>(scratch + (b * G + g) * 512 + 4 * d);
-            a0[g] += wb * v.x;
-            a1[g] += wb * v.y;
-          }
-        }
-      }
-      wave_lds_fence();
+    const float lse = k0 == 0 ? lse0 : (k < n ? p.part_lse[slot(k)] : -INFINITY);
+    const float w = (k < n && mx != -INFINITY) ? fast_exp2(lse - mx) : 0.f;
+    wsum += w;
+    const int cnt = min(64, n - k0);
+#pragma unroll 8
+    for (int j = 0; j < cnt; ++j) {
+      const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), j));
+      const f32x2 val = *reinterpret_cast<const f32x2*>(p.part_o + slot(k0 + j) * kHeadDim + 2 * lane);
+      a0 += wj * val.x;
+      a1 += wj * val.y;
     }
   }
 #pragma unroll
-  for (int g = 0; g < 16; ++g) {
-    if (g < G) {
-      float ws = wsum[g];
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) ws += __shfl_xor(ws, off);
-      const float winv = ws > 0.f ? 1.0f / ws : 0.f;
-      T* op = (T*)p.out + qrow * p.out_tok_stride + (int64_t)(h * G + g) * p.out_head_stride + d;
-      op[0] = (T)(a0[g] * winv);
-      op[1] = (T)(a1[g] * winv);
-    }
-  }
-  if (lane == 0)
-    __hip_atomic_store(&p.counters[(int64_t)s * Hkv + h], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // Leave no store outstanding: the decode loop's waits assume none is.
-  __builtin_amdgcn_s_waitcnt(kVmcnt0);
+  for (int off = 32; off > 0; off >>= 1) wsum += __shfl_xor(wsum, off);
+  const float winv = wsum > 0.f ? 1.0f / wsum : 0.f;
+  T* op = (T*)p.out + qrow * p.out_tok_stride + (int64_t)(h * G + g) * p.out_head_stride + 2 * lane;
+  op[0] = (T)(a0 * winv);
+  op[1] = (T)(a1 * winv);
 }
 
 }  // namespace mva

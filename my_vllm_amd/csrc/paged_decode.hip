@@ -12,22 +12,47 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
   decode_wave<T>(p, (int)blockIdx.x, (lds_u8*)lds);
 }
 
+// Split-K merges: four wavefronts per workgroup, one per (merge entry,
+// query head).
+template <typename T>
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, const int32_t* __restrict__ merges,
+                                                           int64_t num_waves) {
+  const int64_t v = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (v >= num_waves) return;
+  decode_merge_wave<T>(p, merges, v);
+}
+
 }  // namespace
+
+// Launches the split-K merge kernel after a decode (or MIXED) launch on the
+// same stream; `merges` lists the split segments (piece descriptors).
+int launch_decode_merge(const DecodeParams& p, const int32_t* merges, int64_t num_merges, int dtype,
+                        hipStream_t stream) {
+  if (num_merges == 0) return 0;
+  const int64_t waves = num_merges * p.group;
+  const int64_t blocks = (waves + 3) / 4;
+  if (blocks > 0x7fffffffLL) return set_error("paged attention: too many split-K merges");
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(decode_merge_kernel<__bf16>, dim3((uint32_t)blocks), dim3(256), 0, stream, p, merges, waves);
+  else
+    hipLaunchKernelGGL(decode_merge_kernel<_Float16>, dim3((uint32_t)blocks), dim3(256), 0, stream, p, merges, waves);
+  return check_launch("decode_merge");
+}
 
 static int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
-// Workspace layout: [scheduler (kDecodeSchedBytes)][counters int32 num_seqs*Hkv]
-// [lse f32 slots*Hkv*G][o f32 slots*Hkv*G*D].
-int64_t decode_workspace_bytes(int64_t num_seqs, int64_t slots, int hkv, int group) {
-  return kDecodeSchedBytes + align256(num_seqs * hkv * 4) + align256(slots * hkv * group * 4) +
-         align256(slots * hkv * group * kHeadDim * 4);
+// Workspace layout: [scheduler (kDecodeSchedBytes)][lse f32 slots*Hkv*G]
+// [o f32 slots*Hkv*G*D].
+int64_t decode_workspace_bytes(int64_t slots, int hkv, int group) {
+  return kDecodeSchedBytes + align256(slots * hkv * group * 4) + align256(slots * hkv * group * kHeadDim * 4);
 }
 
 int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, int64_t q_head_stride,
                        const void* k_cache, const void* v_cache, int64_t num_pages, int64_t page_stride,
                        int64_t token_stride, const int32_t* block_tables, int64_t block_table_stride,
                        const int32_t* seq_lens, const int32_t* items, int64_t num_items, int64_t num_waves,
-                       int64_t num_seqs, int64_t num_part_slots, void* out, int64_t out_token_stride,
+                       const int32_t* merges, int64_t num_merges, int64_t num_part_slots, void* out,
+                       int64_t out_token_stride,
                        int64_t out_head_stride, void* workspace, int64_t workspace_bytes,
                        int num_q_heads, int num_kv_heads, int head_dim, int page_size,
                        float softmax_scale) {
@@ -41,6 +66,8 @@ int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, i
   if (num_waves < 0 || num_waves > 0x7fffffffLL) return set_error("paged attention: invalid wave count");
   if (num_items > 0 && (num_waves <= 0 || num_waves > num_items))
     return set_error("paged attention: num_waves must be in [1, num_items]");
+  if (num_merges < 0 || num_merges > num_items) return set_error("paged attention: invalid merge count");
+  if (num_merges > 0 && merges == nullptr) return set_error("paged attention: missing merge list");
   if (num_pages <= 0) return set_error("paged attention: empty KV cache");
   const uint64_t align_bits = (uint64_t)(uintptr_t)q | (uint64_t)(uintptr_t)k_cache |
                               (uint64_t)(uintptr_t)v_cache | (uint64_t)(q_token_stride * 2) |
@@ -49,7 +76,8 @@ int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, i
   if (align_bits % 16) return set_error("paged attention: q / cache buffers and strides must be 16-byte aligned");
   if (((uint64_t)(uintptr_t)out | (uint64_t)(out_token_stride * 2) | (uint64_t)(out_head_stride * 2)) % 8)
     return set_error("paged attention: output buffer and strides must be 8-byte aligned");
-  if (workspace_bytes < decode_workspace_bytes(num_seqs, num_part_slots, num_kv_heads, group))
+  if (num_part_slots < 0) return set_error("paged attention: invalid partial slot count");
+  if (workspace_bytes < decode_workspace_bytes(num_part_slots, num_kv_heads, group))
     return set_error("paged attention: workspace too small");
   if (num_items > 0 && workspace == nullptr) return set_error("paged attention: missing workspace");
   p.q = q;
@@ -72,8 +100,6 @@ int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, i
   uint8_t* ws = (uint8_t*)workspace;
   p.sched = (int32_t*)ws;
   ws += kDecodeSchedBytes;
-  p.counters = (int32_t*)ws;
-  ws += align256(num_seqs * num_kv_heads * 4);
   p.part_lse = (float*)ws;
   ws += align256(num_part_slots * num_kv_heads * group * 4);
   p.part_o = (float*)ws;
@@ -85,9 +111,9 @@ int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, i
 
 }  // namespace mva
 
-extern "C" int64_t mva_decode_workspace_bytes(int64_t num_seqs, int64_t num_part_slots,
-                                              int num_kv_heads, int group) {
-  return mva::decode_workspace_bytes(num_seqs, num_part_slots, num_kv_heads, group);
+extern "C" int64_t mva_decode_workspace_bytes(int64_t num_part_slots, int num_kv_heads, int group) {
+  if (num_part_slots < 0 || num_kv_heads <= 0 || group <= 0) return -1;
+  return mva::decode_workspace_bytes(num_part_slots, num_kv_heads, group);
 }
 
 extern "C" int mva_paged_decode(const void* q, int64_t q_token_stride, int64_t q_head_stride,
@@ -95,7 +121,7 @@ extern "C" int mva_paged_decode(const void* q, int64_t q_token_stride, int64_t q
                                 int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
                                 int64_t block_table_stride, const int32_t* seq_lens,
                                 const int32_t* items, int64_t num_items, int64_t num_waves,
-                                int64_t num_seqs,
+                                const int32_t* merges, int64_t num_merges,
                                 int64_t num_part_slots, void* out, int64_t out_token_stride,
                                 int64_t out_head_stride, void* workspace, int64_t workspace_bytes,
                                 int num_q_heads, int num_kv_heads, int head_dim, int page_size,
@@ -104,7 +130,7 @@ extern "C" int mva_paged_decode(const void* q, int64_t q_token_stride, int64_t q
   DecodeParams p;
   int rc = fill_decode_params(p, q, q_token_stride, q_head_stride, k_cache, v_cache, num_pages,
                               page_stride, token_stride, block_tables, block_table_stride, seq_lens,
-                              items, num_items, num_waves, num_seqs, num_part_slots, out,
+                              items, num_items, num_waves, merges, num_merges, num_part_slots, out,
                               out_token_stride,
                               out_head_stride, workspace, workspace_bytes, num_q_heads, num_kv_heads,
                               head_dim, page_size, softmax_scale);
@@ -115,5 +141,7 @@ extern "C" int mva_paged_decode(const void* q, int64_t q_token_stride, int64_t q
   if (dtype == kBF16) hipLaunchKernelGGL(paged_decode_kernel<__bf16>, grid, dim3(64), 0, s, p);
   else if (dtype == kF16) hipLaunchKernelGGL(paged_decode_kernel<_Float16>, grid, dim3(64), 0, s, p);
   else return set_error("paged attention: dtype must be bf16 or fp16");
-  return check_launch("paged_decode");
+  rc = check_launch("paged_decode");
+  if (rc) return rc;
+  return launch_decode_merge(p, merges, num_merges, dtype, s);
 }

@@ -5,15 +5,17 @@
 
 namespace mva {
 
-int64_t decode_workspace_bytes(int64_t num_seqs, int64_t slots, int hkv, int group);
 int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, int64_t q_head_stride,
                        const void* k_cache, const void* v_cache, int64_t num_pages, int64_t page_stride,
                        int64_t token_stride, const int32_t* block_tables, int64_t block_table_stride,
                        const int32_t* seq_lens, const int32_t* items, int64_t num_items, int64_t num_waves,
-                       int64_t num_seqs, int64_t num_part_slots, void* out, int64_t out_token_stride,
+                       const int32_t* merges, int64_t num_merges, int64_t num_part_slots, void* out,
+                       int64_t out_token_stride,
                        int64_t out_head_stride, void* workspace, int64_t workspace_bytes,
                        int num_q_heads, int num_kv_heads, int head_dim, int page_size,
                        float softmax_scale);
+int launch_decode_merge(const DecodeParams& p, const int32_t* merges, int64_t num_merges, int dtype,
+                        hipStream_t stream);
 
 namespace {
 
@@ -162,8 +164,8 @@ extern "C" int mva_paged_mixed(const void* q, int64_t q_token_stride, int64_t q_
                                int64_t block_table_stride, const int32_t* seq_lens,
                                const int32_t* query_start_loc, const int32_t* prefill_items,
                                int64_t num_prefill_items, const int32_t* decode_items,
-                               int64_t num_decode_items, int64_t num_decode_waves, int64_t num_seqs,
-                               int64_t num_part_slots,
+                               int64_t num_decode_items, int64_t num_decode_waves,
+                               const int32_t* decode_merges, int64_t num_decode_merges, int64_t num_part_slots,
                                void* out, int64_t out_token_stride, int64_t out_head_stride,
                                void* workspace, int64_t workspace_bytes, int num_q_heads,
                                int num_kv_heads, int head_dim, int page_size, float softmax_scale,
@@ -178,7 +180,7 @@ extern "C" int mva_paged_mixed(const void* q, int64_t q_token_stride, int64_t q_
   DecodeParams dp;
   rc = fill_decode_params(dp, q, q_token_stride, q_head_stride, k_cache, v_cache, num_pages, page_stride,
                           token_stride, block_tables, block_table_stride, seq_lens, decode_items,
-                          num_decode_items, num_decode_waves, num_seqs, num_part_slots, out,
+                          num_decode_items, num_decode_waves, decode_merges, num_decode_merges, num_part_slots, out,
                           out_token_stride, out_head_stride,
                           workspace, workspace_bytes, num_q_heads, num_kv_heads, head_dim, page_size,
                           softmax_scale);
@@ -195,5 +197,7 @@ extern "C" int mva_paged_mixed(const void* q, int64_t q_token_stride, int64_t q_
   else if (dtype == kF16)
     hipLaunchKernelGGL(paged_mixed_kernel<_Float16>, grid, dim3(256), 0, s, pp, dp, np, nd);
   else return set_error("paged attention: dtype must be bf16 or fp16");
-  return check_launch("paged_mixed");
+  rc = check_launch("paged_mixed");
+  if (rc) return rc;
+  return launch_decode_merge(dp, decode_merges, num_decode_merges, dtype, s);
 }

@@ -121,10 +121,22 @@ def store_kvcache(
     )
 
 
-def decode_workspace_bytes(num_seqs: int, num_part_slots: int, num_kv_heads: int, group: int) -> int:
-    return int(
-        _native.query("mva_decode_workspace_bytes", num_seqs, num_part_slots, num_kv_heads, group)
-    )
+def decode_workspace_bytes(num_part_slots: int, num_kv_heads: int, group: int) -> int:
+    """Workspace bytes of a decode (or MIXED) launch with ``num_part_slots`` split-K slots."""
+    nbytes = int(_native.query("mva_decode_workspace_bytes", num_part_slots, num_kv_heads, group))
+    if nbytes < 0:
+        raise ValueError("invalid decode workspace arguments")
+    return nbytes
+
+
+def decode_merge_list(items):
+    """The merge entries of a decode plan: chunk 0 of every split segment.
+
+    ``items`` is the int32 ``[n, 8]`` piece array (numpy); the result has the
+    same format and lists each (sequence, KV head) cut into more than one
+    piece exactly once.
+    """
+    return items[(items[:, 3] == 0) & (items[:, 4] > 1)]
 
 
 def paged_decode(
@@ -136,7 +148,8 @@ def paged_decode(
     items: torch.Tensor,
     num_items: int,
     num_waves: int,
-    num_seqs: int,
+    merges: torch.Tensor | None,
+    num_merges: int,
     num_part_slots: int,
     out: torch.Tensor,
     workspace: torch.Tensor | None,
@@ -146,7 +159,9 @@ def paged_decode(
 
     ``q``/``out`` are ``[T, Hq, D]`` views (rows addressed by the pieces'
     ``q_row``); caches ``[P, page, Hkv, D]``; ``items`` int32 ``[n, 8]``,
-    claimed by ``num_waves`` (``1 <= num_waves <= n``) wavefronts.
+    claimed by ``num_waves`` (``1 <= num_waves <= n``) wavefronts;
+    ``merges`` (see :func:`decode_merge_list`) lists the split segments whose
+    partials the follow-up merge kernel combines.
     """
     num_q_heads, head_dim = q.shape[1], q.shape[2]
     num_pages, page_size, num_kv_heads = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
@@ -157,7 +172,8 @@ def paged_decode(
         q.data_ptr(), q.stride(0), q.stride(1),
         k_cache.data_ptr(), v_cache.data_ptr(), num_pages, k_cache.stride(0), k_cache.stride(1),
         block_tables.data_ptr(), block_tables.stride(0), seq_lens.data_ptr(),
-        items.data_ptr(), num_items, num_waves, num_seqs, num_part_slots,
+        items.data_ptr(), num_items, num_waves,
+        merges.data_ptr() if merges is not None else 0, num_merges, num_part_slots,
         out.data_ptr(), out.stride(0), out.stride(1),
         ws_ptr, ws_bytes,
         num_q_heads, num_kv_heads, head_dim, page_size, float(softmax_scale),
@@ -219,7 +235,8 @@ def paged_mixed(
     decode_items: torch.Tensor | None,
     num_decode_items: int,
     num_decode_waves: int,
-    num_seqs: int,
+    decode_merges: torch.Tensor | None,
+    num_decode_merges: int,
     num_part_slots: int,
     out: torch.Tensor,
     workspace: torch.Tensor | None,
@@ -234,7 +251,7 @@ def paged_mixed(
         query_start_loc.data_ptr(),
         prefill_items.data_ptr(), num_prefill_items,
         decode_items.data_ptr() if decode_items is not None else 0, num_decode_items, num_decode_waves,
-        num_seqs, num_part_slots,
+        decode_merges.data_ptr() if decode_merges is not None else 0, num_decode_merges, num_part_slots,
         out.data_ptr(), out.stride(0), out.stride(1),
         ws_ptr, ws_bytes,
         *_tail_args(q, k_cache, softmax_scale),

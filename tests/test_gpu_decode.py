@@ -88,7 +88,7 @@ def test_split_k_merge(gpu, monkeypatch, waves):
     expected = _expected(batch)
     assert_attention_close(out, expected)
     first = out.clone()
-    # Counters are reset by the merging wave: a second launch is identical.
+    # The last wavefront resets the claim counters: a second launch is identical.
     q, kc, vc, empty = args
     again = backend.forward(q, empty, empty, kc, vc, plan)
     assert torch.equal(again, first)
@@ -98,7 +98,7 @@ def test_split_k_merge(gpu, monkeypatch, waves):
 def test_piece_plans_through_c_abi(gpu, waves, per_wave, min_pages):
     # One-page pieces, one-page sequences and single-piece wavefronts exercise
     # every branch of the page stream across piece boundaries; a second launch
-    # checks that the scheduler and arrival counters were reset.
+    # checks that the claim counters were reset.
     ctx = [1, 16, 17, 40, 1, 300, 33, 2049, 5, 640]
     hq, hkv = 32, 8
     batch = make_paged_batch(61, [1] * len(ctx), ctx, 0, hq, hkv)
@@ -106,11 +106,12 @@ def test_piece_plans_through_c_abi(gpu, waves, per_wave, min_pages):
     counts = np.asarray([(n + 15) // 16 for n in ctx])
     items, nw, slots = make_decode_plan(counts, 0, 0, hkv, waves, per_wave, min_pages)
     assert nw == min(waves, items.shape[0])
-    ws = torch.zeros(ops.decode_workspace_bytes(len(ctx), slots, hkv, hq // hkv), dtype=torch.uint8, device=gpu)
+    ws = torch.zeros(ops.decode_workspace_bytes(slots, hkv, hq // hkv), dtype=torch.uint8, device=gpu)
     out = torch.full_like(q, float("nan"))
     scale = 128 ** -0.5
+    merges = ops.decode_merge_list(items)
     args = (q, kc, vc, common.block_tables, common.seq_lens, _to_device(items, gpu), items.shape[0], nw,
-            len(ctx), slots, out, ws, scale)
+            _to_device(merges, gpu), merges.shape[0], slots, out, ws, scale)
     ops.paged_decode(*args)
     first = out.clone()
     assert_attention_close(first, _expected(batch))
@@ -131,10 +132,11 @@ def test_merge_of_one_page_pieces_for_every_group_shape(gpu, hq, hkv):
     counts = np.asarray([(n + 15) // 16 for n in ctx])
     items, nw, slots = make_decode_plan(counts, 0, 0, hkv, 5000, 64, 1)
     assert int(items[:, 4].max()) == 129
-    ws = torch.zeros(ops.decode_workspace_bytes(len(ctx), slots, hkv, hq // hkv), dtype=torch.uint8, device=gpu)
+    ws = torch.zeros(ops.decode_workspace_bytes(slots, hkv, hq // hkv), dtype=torch.uint8, device=gpu)
     out = torch.full_like(q, float("nan"))
+    merges = ops.decode_merge_list(items)
     args = (q, kc, vc, common.block_tables, common.seq_lens, _to_device(items, gpu), items.shape[0], nw,
-            len(ctx), slots, out, ws, 128 ** -0.5)
+            _to_device(merges, gpu), merges.shape[0], slots, out, ws, 128 ** -0.5)
     ops.paged_decode(*args)
     first = out.clone()
     assert_attention_close(first, _expected(batch))

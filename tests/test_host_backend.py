@@ -263,3 +263,19 @@ def test_prefill_items_cover_every_tile_once(seed):
     cost = [int(kv_ub[s] - q_ub[s] + min(t + tile, q_ub[s])) for s, t in items[:, :2]]
     assert all(a >= b for a, b, sa, sb in zip(cost, cost[1:], seqs, seqs[1:]) if sa == sb), \
         "largest key count first within a sequence"
+
+
+@pytest.mark.parametrize("seed", range(5))
+def test_decode_merge_list_names_every_split_segment_once(seed):
+    rng = np.random.default_rng(300 + seed)
+    counts = rng.integers(1, 300, size=int(rng.integers(1, 30)))
+    hkv = int(rng.choice([1, 4, 8]))
+    items, _, slots = make_decode_plan(counts, 3, 7, hkv, int(rng.choice([16, 256, 4096])), 2.0, 1)
+    merges = ops.decode_merge_list(items)
+    assert merges.dtype == np.int32 and merges.shape[1] == ops.DECODE_ITEM_INTS
+    split = {(int(s), int(h)) for s, n, h in items[:, [0, 4, 7]] if n > 1}
+    listed = [(int(s), int(h)) for s, h in merges[:, [0, 7]]]
+    assert len(listed) == len(set(listed)) and set(listed) == split
+    assert np.all(merges[:, 3] == 0) and np.all(merges[:, 4] > 1)
+    # Every merge's slots stay inside the plan's partial-slot count.
+    assert np.all(merges[:, 5] + merges[:, 4] <= slots)

@@ -35,7 +35,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     lib = _native.load_library()
     for name in _declared_functions():
         assert hasattr(lib, name), f"{name} missing from {_native.LIB_PATH.name}"
-    assert lib.mva_abi_version() == 1
+    assert lib.mva_abi_version() == 2
 
 
 def test_library_binds_to_the_process_hip_runtime():
@@ -52,9 +52,10 @@ def test_host_queries():
     assert _native.query("mva_prefill_tile_tokens", 32, 8) == 32
     assert _native.query("mva_prefill_tile_tokens", 64, 8) == 16
     assert _native.query("mva_prefill_tile_tokens", 12, 5) == -1
-    small = _native.query("mva_decode_workspace_bytes", 4, 0, 8, 2)
-    big = _native.query("mva_decode_workspace_bytes", 4, 100, 8, 2)
+    small = _native.query("mva_decode_workspace_bytes", 0, 8, 2)
+    big = _native.query("mva_decode_workspace_bytes", 100, 8, 2)
     assert small > 0 and big > small and big % 256 == 0
+    assert _native.query("mva_decode_workspace_bytes", -1, 8, 2) == -1
 
 
 def test_invalid_arguments_fail_before_launch_with_a_message():
@@ -64,7 +65,7 @@ def test_invalid_arguments_fail_before_launch_with_a_message():
     assert lib.mva_last_error().decode()
     # head_dim 64 is rejected by the decode entry point before anything runs.
     with pytest.raises(RuntimeError, match="mva_paged_decode failed"):
-        _native.call("mva_paged_decode", 0, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0, 1, 1, 1, 0, 0, 0, 0, 0, 0,
+        _native.call("mva_paged_decode", 0, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0, 1, 1, 0, 0, 0, 0, 0, 0, 0, 0,
                      16, 8, 64, 16, 1.0, 0, 0)
 
 
