@@ -587,7 +587,8 @@ __device__ void decode_merge_wave(const DecodeParams& p, const int32_t* __restri
   const int lane = threadIdx.x & 63;
   const int G = p.group;
   const int Hkv = p.num_kv_heads;
-  const int32_t* d = merges + (v / G) * kDecodeItemInts;
+  // v is wave-uniform: the descriptor comes in through scalar loads.
+  const i32x8 d = ((const_i32x8*)merges)[v / G];
   const int g = (int)(v % G);
   const int n = d[4];
   const int pbase = d[5];
@@ -595,6 +596,14 @@ __device__ void decode_merge_wave(const DecodeParams& p, const int32_t* __restri
   const int h = d[7];
   // Partial slot of chunk k (lse index; o row = slot * D).
   auto slot = [&](int k) -> int64_t { return ((int64_t)(pbase + k) * Hkv + h) * G + g; };
+  // The first 16 chunks' rows are requested together with the log-sum-exps
+  // (they do not depend on the weights), so a merge of up to 16 chunks costs
+  // one memory round trip.  Chunk indices past n are clamped (weight 0).
+  constexpr int kBatch = 16;
+  f32x2 rows[kBatch];
+#pragma unroll
+  for (int j = 0; j < kBatch; ++j)
+    rows[j] = *reinterpret_cast<const f32x2*>(p.part_o + slot(min(j, n - 1)) * kHeadDim + 2 * lane);
   float lse0 = lane < n ? p.part_lse[slot(lane)] : -INFINITY;  // chunks 0..63, kept for the weights
   float mx = lse0;
   for (int k0 = 64; k0 < n; k0 += 64)
@@ -608,12 +617,22 @@ __device__ void decode_merge_wave(const DecodeParams& p, const int32_t* __restri
     const float w = (k < n && mx != -INFINITY) ? fast_exp2(lse - mx) : 0.f;
     wsum += w;
     const int cnt = min(64, n - k0);
-#pragma unroll 8
-    for (int j = 0; j < cnt; ++j) {
-      const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), j));
-      const f32x2 val = *reinterpret_cast<const f32x2*>(p.part_o + slot(k0 + j) * kHeadDim + 2 * lane);
-      a0 += wj * val.x;
-      a1 += wj * val.y;
+    for (int j0 = 0; j0 < cnt; j0 += kBatch) {
+      if (k0 + j0 > 0) {
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j)
+          rows[j] = *reinterpret_cast<const f32x2*>(p.part_o + slot(min(k0 + j0 + j, n - 1)) * kHeadDim + 2 * lane);
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        // Lanes past the chunk count hold weight 0; the clamped rows they
+        // pair with are finite partials.
+        const float wj =
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), min(j0 + j, 63)));
+        const float wk = j0 + j < cnt ? wj : 0.f;
+        a0 += wk * rows[j].x;
+        a1 += wk * rows[j].y;
+      }
     }
   }
 #pragma unroll

@@ -17,7 +17,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
 template <typename T>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, const int32_t* __restrict__ merges,
                                                            int64_t num_waves) {
-  const int64_t v = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t v = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (v >= num_waves) return;
   decode_merge_wave<T>(p, merges, v);
 }
