@@ -148,7 +148,7 @@ def headline(args, device):
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": measured_traffic(),
-            "kernel": "paged_decode_kernel<bf16>",
+            "kernel": "paged_decode_kernel<bf16> + decode_merge_kernel<bf16> (one mva_paged_decode call)",
             "bytes_per_launch": dec_bytes,
             "avg_launch_ms": round(ms_decode, 5),
         },
