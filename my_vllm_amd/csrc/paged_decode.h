@@ -122,7 +122,7 @@ __device__ inline int sload(const int32_t* base, int64_t idx) { return ((const_i
 // Per-iteration memory work of a decode wavefront, issued as one asm
 // statement, in this order:
 //   * lane 0: claim = atomic_add(claim_ptr, 1) if `claiming`;
-//   * all lanes, if `claiming`: the next piece's page-table words
+//   * all lanes, if `loading`: the next piece's page-table words
 //     (bt0 -> bt_lo, bt1 -> bt_hi) and query fragments (q .. q + 63 -> qv);
 //   * if kDma: the 8 DMAs of one page of one KV head (4 to lds_v, 4 to
 //     lds_k, 1 KB each), then s_waitcnt vmcnt(8), which retires everything
@@ -133,7 +133,7 @@ __device__ inline int sload(const int32_t* base, int64_t idx) { return ((const_i
 // so DMA i holds d-chunks 4i..4i+3 of all 16 tokens.  The K A-operand read
 // (16 tokens at one chunk) and the V transposed read (4 tokens x 2 chunks
 // per 16-lane group) both cover whole 256-byte bank rows.
-// `claiming` is wave-uniform.  Outputs not issued keep their previous
+// `loading` and `claiming` are wave-uniform.  Outputs not issued keep their previous
 // contents (claim: unspecified).
 struct DecodeStepIo {
   int claim;
@@ -143,11 +143,12 @@ struct DecodeStepIo {
 };
 
 template <bool kDma>
-__device__ inline void decode_step(DecodeStepIo& io, int claiming, int* claim_ptr, const int32_t* bt0, const int32_t* bt1, const void* q, const void* v_src,
+__device__ inline void decode_step(DecodeStepIo& io, int loading, int claiming, int* claim_ptr, const int32_t* bt0, const int32_t* bt1, const void* q, const void* v_src,
                                    const void* k_src, uint32_t lds_v, uint32_t lds_k) {
   uint64_t saved;
   uint32_t m0_saved;
   const int on_c = __builtin_amdgcn_readfirstlane(claiming != 0 ? 1 : 0);
+  const int on_y = __builtin_amdgcn_readfirstlane(loading != 0 ? 1 : 0);
   lds_v = __builtin_amdgcn_readfirstlane(lds_v);
   lds_k = __builtin_amdgcn_readfirstlane(lds_k);
   const char* v = (const char*)v_src;
@@ -158,7 +159,7 @@ __device__ inline void decode_step(DecodeStepIo& io, int claiming, int* claim_pt
         "s_mov_b32 exec_lo, %[onc]\n\t"
         "s_mov_b32 exec_hi, 0\n\t"
         "global_atomic_add %[cl], %[cp], %[one], off sc0\n\t"
-        "s_cmp_eq_u32 %[onc], 0\n\t"
+        "s_cmp_eq_u32 %[ony], 0\n\t"
         "s_cselect_b64 exec, 0, %[sv]\n\t"
         "global_load_dword %[blo], %[b0], off\n\t"
         "global_load_dword %[bhi], %[b1], off\n\t"
@@ -197,7 +198,7 @@ __device__ inline void decode_step(DecodeStepIo& io, int claiming, int* claim_pt
         : [cl] "=&v"(io.claim), [blo] "+v"(io.bt_lo), [bhi] "+v"(io.bt_hi),
           [q0] "+v"(io.qv[0]), [q1] "+v"(io.qv[1]), [q2] "+v"(io.qv[2]), [q3] "+v"(io.qv[3]), [sv] "=&s"(saved),
           [m0s] "=&s"(m0_saved)
-        : [onc] "s"(on_c), [cp] "v"(claim_ptr), [one] "v"(1),
+        : [onc] "s"(on_c), [ony] "s"(on_y), [cp] "v"(claim_ptr), [one] "v"(1),
           [b0] "v"(bt0), [b1] "v"(bt1), [qp] "v"(q), [lv] "s"(lds_v), [lk] "s"(lds_k), [v0] "v"(v),
           [v1] "v"(v + 64), [v2] "v"(v + 128), [v3] "v"(v + 192), [k0] "v"(k), [k1] "v"(k + 64),
           [k2] "v"(k + 128), [k3] "v"(k + 192)
@@ -208,7 +209,7 @@ __device__ inline void decode_step(DecodeStepIo& io, int claiming, int* claim_pt
         "s_mov_b32 exec_lo, %[onc]\n\t"
         "s_mov_b32 exec_hi, 0\n\t"
         "global_atomic_add %[cl], %[cp], %[one], off sc0\n\t"
-        "s_cmp_eq_u32 %[onc], 0\n\t"
+        "s_cmp_eq_u32 %[ony], 0\n\t"
         "s_cselect_b64 exec, 0, %[sv]\n\t"
         "global_load_dword %[blo], %[b0], off\n\t"
         "global_load_dword %[bhi], %[b1], off\n\t"
@@ -220,7 +221,7 @@ __device__ inline void decode_step(DecodeStepIo& io, int claiming, int* claim_pt
         "s_waitcnt vmcnt(0)"
         : [cl] "=&v"(io.claim), [blo] "+v"(io.bt_lo), [bhi] "+v"(io.bt_hi),
           [q0] "+v"(io.qv[0]), [q1] "+v"(io.qv[1]), [q2] "+v"(io.qv[2]), [q3] "+v"(io.qv[3]), [sv] "=&s"(saved)
-        : [onc] "s"(on_c), [cp] "v"(claim_ptr), [one] "v"(1),
+        : [onc] "s"(on_c), [ony] "s"(on_y), [cp] "v"(claim_ptr), [one] "v"(1),
           [b0] "v"(bt0), [b1] "v"(bt1), [qp] "v"(q)
         : "memory", "scc");
   }
@@ -429,7 +430,7 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
     const int64_t base = (int64_t)page_of(bt_lo, bt_hi, 0) * p.page_stride + X[7] * kHeadDim;
     const int64_t lane_off = (lane & 15) * p.tok_stride + 8 * (lane >> 4);
     const uint32_t lds_k = (uint32_t)(uintptr_t)lds;
-    decode_step<true>(io, 0, claim_ctr, bt_word(X, lane), bt_word(X, 64 + lane), q_addr(X),
+    decode_step<true>(io, 0, 0, claim_ctr, bt_word(X, lane), bt_word(X, 64 + lane), q_addr(X),
                       (const T*)p.v_cache + base + lane_off, (const T*)p.k_cache + base + lane_off,
                       lds_k + kDecodePageBytes, lds_k);
   }
@@ -472,17 +473,19 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
 
     // One asm statement issues Y's page table and queries and the claim for
     // Z (first page of X) and the next page's DMAs, then waits for all of it
-    // but those DMAs (see decode_step).
-    const int claiming = (i == 0 && yi < N) ? 1 : 0;
+    // but those DMAs (see decode_step).  When the two static rounds cover
+    // every piece (N <= 2W) there is nothing to claim.
+    const int loading = (i == 0 && yi < N) ? 1 : 0;
+    const int claiming = (loading && 2 * W < N) ? 1 : 0;
     if (fvalid) {
       const int64_t base = (int64_t)fpg * p.page_stride + fh * kHeadDim;
       const int64_t lane_off = (lane & 15) * p.tok_stride + 8 * (lane >> 4);
       const uint32_t lds_k = (uint32_t)(uintptr_t)nxt;
-      decode_step<true>(io, claiming, claim_ctr, bt_word(Y, lane), bt_word(Y, 64 + lane),
+      decode_step<true>(io, loading, claiming, claim_ctr, bt_word(Y, lane), bt_word(Y, 64 + lane),
                         q_addr(Y), (const T*)p.v_cache + base + lane_off, (const T*)p.k_cache + base + lane_off,
                         lds_k + kDecodePageBytes, lds_k);
     } else {
-      decode_step<false>(io, claiming, claim_ctr, bt_word(Y, lane), bt_word(Y, 64 + lane), q_addr(Y), nullptr,
+      decode_step<false>(io, loading, claiming, claim_ctr, bt_word(Y, lane), bt_word(Y, 64 + lane), q_addr(Y), nullptr,
                          nullptr, 0, 0);
     }
     wave_lds_fence();
@@ -562,13 +565,14 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
   // retired by the wait of the iteration that issued it), so all claims
   // precede the reset.
   __builtin_amdgcn_s_waitcnt(kVmcnt0);
-  if (lane == 0) {
-    int* const exit_ctr = p.sched + kDecodeClaimCounters * kDecodeSchedLineInts;
-    const int gone = __hip_atomic_fetch_add(exit_ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (gone == W - 1) {
-      for (int k = 0; k < C; ++k)
-        __hip_atomic_store(p.sched + k * kDecodeSchedLineInts, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(exit_ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  int* const exit_ctr = p.sched + kDecodeClaimCounters * kDecodeSchedLineInts;
+  int gone = 0;
+  if (lane == 0) gone = __hip_atomic_fetch_add(exit_ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (__builtin_amdgcn_readfirstlane(gone) == W - 1) {
+    // Lane k < C clears claim counter k; lane C clears the exit counter.
+    if (lane <= C) {
+      int* const ctr = lane < C ? p.sched + lane * kDecodeSchedLineInts : exit_ctr;
+      __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
