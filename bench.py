@@ -131,7 +131,8 @@ def headline(args, device):
         kc, vc = caches[i % copies]
         ops.paged_decode(q, kc, vc, md.block_tables, md.seq_lens, md.decode_items, md.num_decode_items,
                          md.num_decode_waves, md.decode_merges, md.num_decode_merges,
-                         md.num_decode_part_slots, out, ws, backend.softmax_scale)
+                         md.num_decode_part_slots, out, ws, backend.softmax_scale,
+                         md.decode_wave_extra, md.decode_waves_per_group)
 
     ms_decode = time_launches(decode_only, max(args.steps, 200), args.warmup)
     dec_bytes = decode_bytes(batch, hq, hkv)
@@ -155,6 +156,7 @@ def headline(args, device):
         "batch": batch,
         "waves": md.num_decode_waves,
         "items": md.num_decode_items,
+        "schedule": "piece lists" if md.decode_wave_extra is not None else "claims",
     }
 
 
@@ -309,7 +311,8 @@ def run_only(args, device):
             kc, vc = caches[i % copies]
             ops.paged_decode(q, kc, vc, md.block_tables, md.seq_lens, md.decode_items, md.num_decode_items,
                              md.num_decode_waves, md.decode_merges, md.num_decode_merges,
-                             md.num_decode_part_slots, out, ws, backend.softmax_scale)
+                             md.num_decode_part_slots, out, ws, backend.softmax_scale,
+                             md.decode_wave_extra, md.decode_waves_per_group)
         torch.cuda.synchronize()
         print(json.dumps({"only": args.only, "bytes_per_launch": decode_bytes(batch, hq, hkv), "launches": n,
                           "waves": md.num_decode_waves, "pieces": md.num_decode_items}))
@@ -370,6 +373,7 @@ def main(argv=None):
             "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBPS, 2),
             "decode_waves": head["waves"],
             "decode_pieces": head["items"],
+            "decode_schedule": head["schedule"],
         },
         "roofline": head["roofline"],
         "cpu_baseline": cpu,

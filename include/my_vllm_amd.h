@@ -82,9 +82,18 @@ int64_t mva_decode_workspace_bytes(int64_t num_part_slots, int num_kv_heads, int
  *         (at most 128 pages), piece `chunk` of `n_chunks`; split-K partial
  *         slots part_base .. part_base + n_chunks - 1 (unused when
  *         n_chunks == 1); output row q_row.
- *   num_waves (1 .. num_items): wavefronts launched; wavefront w runs
- *         pieces w and num_waves + w and then claims later pieces from
- *         counters in the workspace, so pieces should be listed longest first.
+ *   num_waves (1 .. num_items): wavefronts launched; wavefront w first runs
+ *         piece w.  Its later pieces follow one of two schedules:
+ *   wave_extra [num_waves + 1] int32, or NULL:
+ *         piece lists: wavefront w then runs pieces wave_extra[w] ..
+ *         wave_extra[w + 1] - 1 in order (num_waves <= wave_extra[w] <=
+ *         wave_extra[w + 1] <= num_items); no workspace counter is touched.
+ *         NULL: wavefront w runs piece num_waves + w and then claims later
+ *         pieces from counters in the workspace, so pieces should be listed
+ *         longest first.
+ *   waves_per_group (1, 2, 4 or 8): wavefronts per workgroup; wavefronts
+ *         g*waves_per_group .. (g+1)*waves_per_group - 1 share a CU.  Must be 1
+ *         when wave_extra is NULL.
  *   merges [num_merges, 8] int32: one piece descriptor (chunk 0) of every
  *         (sequence, KV head) cut into n_chunks > 1 pieces; a second kernel on
  *         `stream` combines each one's partials into its output rows.
@@ -102,7 +111,8 @@ int mva_paged_decode(const void* q, int64_t q_token_stride, int64_t q_head_strid
                      const void* k_cache, const void* v_cache, int64_t num_pages,
                      int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
                      int64_t block_table_stride, const int32_t* seq_lens, const int32_t* items,
-                     int64_t num_items, int64_t num_waves, const int32_t* merges,
+                     int64_t num_items, int64_t num_waves, const int32_t* wave_extra,
+                     int waves_per_group, const int32_t* merges,
                      int64_t num_merges, int64_t num_part_slots, void* out,
                      int64_t out_token_stride, int64_t out_head_stride, void* workspace,
                      int64_t workspace_bytes, int num_q_heads, int num_kv_heads, int head_dim,

@@ -40,6 +40,7 @@ _SIGNATURES = {
             _c_void_p, _c_void_p, _i64, _i64, _i64,  # k_cache, v_cache, num_pages, page_stride, token_stride
             _c_void_p, _i64, _c_void_p,  # block_tables, block_table_stride, seq_lens
             _c_void_p, _i64, _i64,  # items, num_items, num_waves
+            _c_void_p, _i32,  # wave_extra, waves_per_group
             _c_void_p, _i64, _i64,  # merges, num_merges, num_part_slots
             _c_void_p, _i64, _i64,  # out, out_token_stride, out_head_stride
             _c_void_p, _i64,  # workspace, workspace_bytes

@@ -267,9 +267,12 @@ MAX_GROUP = 16
 class MI355XAttentionMetadata:
     """Backend-private per-step metadata: device work lists built on the host.
 
-    ``decode_items`` is int32 ``[num_decode_items, 8]`` pieces, claimed by
-    ``num_decode_waves`` wavefronts (see ``make_decode_plan``); ``None``
-    without decode sequences.  ``decode_merges`` lists the split segments
+    ``decode_items`` is int32 ``[num_decode_items, 8]`` pieces run by
+    ``num_decode_waves`` wavefronts, ``decode_waves_per_group`` to a
+    workgroup; ``None`` without decode sequences.  With
+    ``decode_wave_extra`` (int32 ``[num_decode_waves + 1]``) each wavefront
+    runs its own piece list (``make_decode_plan_listed``); without it the
+    wavefronts claim pieces (``make_decode_plan``).  ``decode_merges`` lists the split segments
     (``ops.decode_merge_list``) whose partials the merge kernel combines.
     ``prefill_items`` is int32 ``[num_prefill_items, 4]`` query tiles (see
     ``make_prefill_items``).  ``kv_indptr`` is the page CSR offset list (host
@@ -288,6 +291,8 @@ class MI355XAttentionMetadata:
     num_decode_part_slots: int = 0
     decode_merges: torch.Tensor | None = None
     num_decode_merges: int = 0
+    decode_wave_extra: torch.Tensor | None = None
+    decode_waves_per_group: int = 1
     prefill_items: torch.Tensor | None = None
     num_prefill_items: int = 0
 
@@ -379,6 +384,116 @@ def make_decode_plan(
     items = items[order]
     waves = max(1, min(int(num_waves), items.shape[0]))
     return items, waves, int(split_sizes.sum())
+
+
+# Workgroups of a piece-list decode launch fill 8 wave slots per CU (the
+# kernel's occupancy is 2 wavefronts per SIMD).
+_LISTED_WAVES_PER_CU = 8
+# Piece lists (an equal share of pages per wavefront, no claims) up to this
+# many K/V bytes per launch; larger batches use claims, whose dynamic
+# balance absorbs the uneven per-CU bandwidth of a long launch.
+_LISTED_MAX_BYTES = 2 << 30
+
+
+def decode_schedule(total_pages: int, num_kv_heads: int, elem_bytes: int = 2) -> str:
+    """"listed" or "claims" for a decode batch of ``total_pages`` pages."""
+    forced = os.environ.get("MVA_DECODE_SCHEDULE")
+    if forced in ("listed", "claims"):
+        return forced
+    kv_bytes = total_pages * PAGE_SIZE * num_kv_heads * HEAD_DIM * elem_bytes * 2
+    return "listed" if kv_bytes <= _LISTED_MAX_BYTES else "claims"
+
+
+def listed_decode_groups(num_kv_heads: int, device: torch.device | None = None) -> tuple[int, int]:
+    """(workgroups, wavefronts per workgroup) of a piece-list decode launch.
+
+    A workgroup holds one wavefront per KV head when the head count divides 8
+    (so one CU streams every head of the same pages), else one wavefront.
+    """
+    per_group = num_kv_heads if num_kv_heads in (1, 2, 4, 8) else 1
+    cus = 256
+    if device is not None and device.type == "cuda":
+        cus = torch.cuda.get_device_properties(device).multi_processor_count
+    override = os.environ.get("MVA_DECODE_WAVES")
+    waves = max(1, int(override)) if override else cus * _LISTED_WAVES_PER_CU
+    return max(1, waves // num_kv_heads), per_group
+
+
+def make_decode_plan_listed(
+    block_counts: np.ndarray | tuple[int, ...],
+    first_seq: int,
+    first_q_row: int,
+    num_kv_heads: int,
+    num_groups: int,
+    max_piece_pages: int = ops.MAX_CHUNK_PAGES,
+) -> tuple[np.ndarray, np.ndarray, int, int]:
+    """An equal share of the batch's pages for every wavefront, as piece lists.
+
+    The pages of all sequences, in batch order, are cut into ``G =
+    min(num_groups, total pages)`` contiguous ranges of near-equal length
+    (range ``g`` = pages ``[g*T//G, (g+1)*T//G)``).  Wavefront ``g*Hkv + h``
+    streams KV head ``h`` of range ``g``: one piece per sequence the range
+    touches (cut further to at most ``max_piece_pages``).  A (sequence, KV
+    head) spread over several pieces is split-K: its pieces are chunks
+    ``0..n-1`` in page order, with partial slots ``part_base .. part_base +
+    n - 1`` shared by the sequence's KV heads (slot ``(part_base + chunk) *
+    Hkv + h``).  Every wavefront gets at least one piece.
+
+    Returns ``(items, wave_extra, waves, num_part_slots)``: items hold the
+    first piece of wavefront ``w`` at row ``w`` and its later pieces, in page
+    order, at rows ``wave_extra[w] .. wave_extra[w + 1] - 1``.
+    """
+    counts = np.asarray(block_counts, dtype=np.int64)
+    if counts.size == 0:
+        return np.zeros((0, ops.DECODE_ITEM_INTS), np.int32), np.zeros(1, np.int32), 0, 0
+    if np.any(counts <= 0):
+        raise ValueError("every decode sequence needs at least one page")
+    if not 1 <= max_piece_pages <= ops.MAX_CHUNK_PAGES:
+        raise ValueError("piece length must be in [1, 128] pages")
+    hkv = int(num_kv_heads)
+    offsets = np.concatenate(([0], np.cumsum(counts)))
+    total = int(offsets[-1])
+    groups = max(1, min(int(num_groups), total))
+    bounds = (np.arange(groups + 1, dtype=np.int64) * total) // groups
+    # Breakpoints of both partitions: every interval lies in one range and
+    # one sequence.
+    cuts = np.union1d(bounds, offsets)
+    starts, ends = cuts[:-1], cuts[1:]
+    group_of = np.searchsorted(bounds, starts, side="right") - 1
+    seq_of = np.searchsorted(offsets, starts, side="right") - 1
+    lengths = ends - starts
+    ncut = (lengths + max_piece_pages - 1) // max_piece_pages
+    iv = np.repeat(np.arange(starts.size), ncut)
+    k = np.arange(iv.size) - np.repeat(np.cumsum(ncut) - ncut, ncut)
+    p_begin = starts[iv] + (k * lengths[iv]) // ncut[iv]
+    p_end = starts[iv] + ((k + 1) * lengths[iv]) // ncut[iv]
+    piece_group = group_of[iv]
+    piece_seq = seq_of[iv]
+    per_seq = np.bincount(piece_seq, minlength=counts.size)
+    chunk = np.arange(iv.size) - (np.cumsum(per_seq) - per_seq)[piece_seq]
+    split = np.where(per_seq > 1, per_seq, 0)
+    part_base = np.cumsum(split) - split
+    pieces = np.zeros((iv.size, hkv, ops.DECODE_ITEM_INTS), dtype=np.int32)
+    pieces[:, :, 0] = (first_seq + piece_seq)[:, None]
+    pieces[:, :, 1] = (p_begin - offsets[piece_seq])[:, None]
+    pieces[:, :, 2] = (p_end - offsets[piece_seq])[:, None]
+    pieces[:, :, 3] = chunk[:, None]
+    pieces[:, :, 4] = per_seq[piece_seq][:, None]
+    pieces[:, :, 5] = part_base[piece_seq][:, None]
+    pieces[:, :, 6] = (first_q_row + piece_seq)[:, None]
+    pieces[:, :, 7] = np.arange(hkv)[None, :]
+    wave_of = (piece_group[:, None] * hkv + np.arange(hkv)[None, :]).reshape(-1)
+    pieces = pieces.reshape(-1, ops.DECODE_ITEM_INTS)
+    order = np.argsort(wave_of, kind="stable")  # page order within a wavefront
+    pieces, wave_of = pieces[order], wave_of[order]
+    waves = groups * hkv
+    per_wave = np.bincount(wave_of, minlength=waves)
+    first = np.cumsum(per_wave) - per_wave
+    is_first = np.zeros(pieces.shape[0], dtype=bool)
+    is_first[first] = True
+    items = np.concatenate([pieces[first], pieces[~is_first]])
+    wave_extra = waves + np.concatenate(([0], np.cumsum(per_wave - 1)))
+    return items, wave_extra.astype(np.int32), waves, int(split.sum())
 
 
 def make_prefill_items(
@@ -571,28 +686,44 @@ class MI355XAttentionBackendMixin:
 
         decode_items = None
         decode_merges = None
+        decode_wave_extra = None
         num_decode_items = 0
         num_decode_merges = 0
         num_decode_waves = 0
         num_part_slots = 0
+        waves_per_group = 1
         if common.num_decode_seqs:
-            waves = resident_decode_waves(
-                block_tables.device, mixed=bool(common.num_prefill_seqs) and self.attention_mode == "unified"
-            )
-            items, num_decode_waves, num_part_slots = make_decode_plan(
-                counts[common.num_prefill_seqs:],
-                common.num_prefill_seqs,
-                common.num_prefill_tokens,
-                self.num_kv_heads,
-                waves,
-            )
+            decode_counts = counts[common.num_prefill_seqs:]
+            one_launch = bool(common.num_prefill_seqs) and self.attention_mode == "unified"
+            wave_extra = None
+            if not one_launch and decode_schedule(int(decode_counts.sum()), self.num_kv_heads) == "listed":
+                groups, waves_per_group = listed_decode_groups(self.num_kv_heads, block_tables.device)
+                items, wave_extra, num_decode_waves, num_part_slots = make_decode_plan_listed(
+                    decode_counts, common.num_prefill_seqs, common.num_prefill_tokens, self.num_kv_heads, groups
+                )
+            else:
+                waves = resident_decode_waves(block_tables.device, mixed=one_launch)
+                items, num_decode_waves, num_part_slots = make_decode_plan(
+                    decode_counts,
+                    common.num_prefill_seqs,
+                    common.num_prefill_tokens,
+                    self.num_kv_heads,
+                    waves,
+                )
             merges = ops.decode_merge_list(items)
             num_decode_items = items.shape[0]
             num_decode_merges = merges.shape[0]
-            # Pieces and merge entries share one host-to-device copy.
-            both = _to_device(np.concatenate([items, merges]), block_tables.device)
-            decode_items = both[:num_decode_items]
-            decode_merges = both[num_decode_items:]
+            # Pieces, merge entries and piece-list offsets share one
+            # host-to-device copy.
+            parts = [items.reshape(-1), merges.reshape(-1)]
+            if wave_extra is not None:
+                parts.append(wave_extra)
+            flat = _to_device(np.concatenate(parts).astype(np.int32), block_tables.device)
+            n_items, n_merge = num_decode_items * ops.DECODE_ITEM_INTS, num_decode_merges * ops.DECODE_ITEM_INTS
+            decode_items = flat[:n_items].view(num_decode_items, ops.DECODE_ITEM_INTS)
+            decode_merges = flat[n_items:n_items + n_merge].view(num_decode_merges, ops.DECODE_ITEM_INTS)
+            if wave_extra is not None:
+                decode_wave_extra = flat[n_items + n_merge:]
         prefill_items = None
         num_prefill_items = 0
         if common.num_prefill_seqs:
@@ -626,6 +757,8 @@ class MI355XAttentionBackendMixin:
             num_decode_part_slots=num_part_slots,
             decode_merges=decode_merges,
             num_decode_merges=num_decode_merges,
+            decode_wave_extra=decode_wave_extra,
+            decode_waves_per_group=waves_per_group,
             prefill_items=prefill_items,
             num_prefill_items=num_prefill_items,
         )
@@ -771,6 +904,8 @@ class MI355XAttentionBackendMixin:
             output,
             workspace,
             self.softmax_scale,
+            metadata.decode_wave_extra,
+            metadata.decode_waves_per_group,
         )
 
     def _run_prefill(self, q, k_cache, v_cache, common, metadata: MI355XAttentionMetadata, output) -> None:

@@ -7,16 +7,24 @@
 //   o = sum_j softmax_j(scale * q . K[j]) V[j]   over j < seq_len,
 // with K/V gathered from NHD pages [P, 16, Hkv, D] through block_tables.
 //
-// Work distribution: the host cuts every (sequence, KV head) into pieces of a
-// few pages (longest first); about one wavefront per resident wave slot is
-// launched.  Wavefront w starts on piece w and then takes pieces from a
-// device-scope counter, so CUs that get more HBM bandwidth simply process
-// more pieces (per-CU bandwidth on a multi-XCD part is uneven enough that an
-// equal static split ends up waiting for the slowest CU).  The next piece's
-// index is claimed one piece ahead and its page table and queries are loaded
-// while the current piece streams, so its first page is in flight before the
-// current piece's epilogue runs.  The last wavefront to exit resets the
-// counters for the next launch.
+// Work distribution, two host-chosen schedules over the same pieces
+// (sequence, KV head, page range):
+//  * piece lists: the host gives every wavefront an equal share of the
+//    batch's pages as an ordered list of pieces (its first piece at index
+//    `wave`, the rest in a per-wave range of the item array).  Launched as
+//    workgroups of Hkv wavefronts, wavefront h of a workgroup streams KV head
+//    h of the workgroup's page range, so one CU reads all heads of a page at
+//    about the same time and no wavefront waits on a shared counter;
+//  * claims: the host cuts every (sequence, KV head) into pieces of a few
+//    pages (longest first); about one wavefront per resident wave slot is
+//    launched.  Wavefront w starts on piece w and then takes pieces from a
+//    device-scope counter, so CUs that get more HBM bandwidth simply process
+//    more pieces (per-CU bandwidth on a multi-XCD part is uneven enough that
+//    an equal static split of a multi-GB batch waits for the slowest CU).
+//    The last wavefront to exit resets the counters for the next launch.
+// Either way the next piece is known one piece ahead and its page table and
+// queries are loaded while the current piece streams, so its first page is
+// in flight before the current piece's epilogue runs.
 //
 // Inside a wavefront:
 //  * The G query heads that share a KV head form the N=16 side of the MFMAs
@@ -76,6 +84,9 @@ struct DecodeParams {
   const int32_t* items;  // [num_items][8], see kDecodeItemInts
   int num_items;
   int num_waves;  // wavefronts in the launch
+  // Piece lists: wavefront w runs piece w, then pieces
+  // [wave_extra[w], wave_extra[w + 1]).  nullptr: the claim schedule.
+  const int32_t* wave_extra;
   int32_t* sched;  // claim counters and exit counter, see kDecodeClaimCounters
   void* out;
   int64_t out_tok_stride;
@@ -249,9 +260,10 @@ static_assert((kDecodeClaimCounters + 1) * kDecodeSchedLineInts * 4 <= kDecodeSc
 // One wavefront of a decode launch (`wave` in [0, num_waves)); `lds` is its
 // kDecodeWaveLdsBytes of LDS.
 //
-// Piece order: wavefront w takes piece w, then piece W + w (W = num_waves),
-// then pieces 2W + C*k + j for k drawn from claim counter j = (w / 8) mod C,
-// C = min(32, max(1, W / 8)).  Blocks are dealt to the 8 XCDs round-robin,
+// Piece order with piece lists: piece w, then wave_extra[w] .. wave_extra[w+1]-1.
+// Piece order with claims: wavefront w takes piece w, then piece W + w (W =
+// num_waves), then pieces 2W + C*k + j for k drawn from claim counter
+// j = (w / 8) mod C, C = min(32, max(1, W / 8)).  Blocks are dealt to the 8 XCDs round-robin,
 // so wavefronts of every XCD share each counter and no counter's share of
 // the queue waits on one slower XCD.  Three pieces are tracked: X (being computed), Y (its
 // successor: descriptor and length known, page table and queries loaded
@@ -304,7 +316,18 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
 
   // ---- piece state --------------------------------------------------------
   i32x8 X = desc_at(wave);
+  // Piece lists: nx is the next unassigned entry of this wavefront's range
+  // [nx, nx_end).
+  const bool listed = p.wave_extra != nullptr;
+  int nx = N, nx_end = N;
   int yi = wave + W;  // >= N: none
+  if (listed) {
+    // Clamped to the item array, so a malformed list cannot index past it.
+    nx = max(sload(p.wave_extra, wave), 0);
+    nx_end = min(sload(p.wave_extra, wave + 1), N);
+    yi = nx < nx_end ? nx : N;
+    ++nx;
+  }
   int zi = N;
   i32x8 Y = X, Z = X;
   if (yi < N) Y = desc_at(yi);
@@ -462,6 +485,8 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
     fvalid = __builtin_amdgcn_readfirstlane(fvalid);
     yi = __builtin_amdgcn_readfirstlane(yi);
     zi = __builtin_amdgcn_readfirstlane(zi);
+    nx = __builtin_amdgcn_readfirstlane(nx);
+    nx_end = __builtin_amdgcn_readfirstlane(nx_end);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       X[k] = __builtin_amdgcn_readfirstlane(X[k]);
@@ -476,7 +501,9 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
     // but those DMAs (see decode_step).  When the two static rounds cover
     // every piece (N <= 2W) there is nothing to claim.
     const int loading = (i == 0 && yi < N) ? 1 : 0;
-    const int claiming = (loading && 2 * W < N) ? 1 : 0;
+    const int claiming = (!listed && loading && 2 * W < N) ? 1 : 0;
+    // Z is assigned now: claimed, or the next entry of this wavefront's list.
+    const int taking = listed ? loading : claiming;
     if (fvalid) {
       const int64_t base = (int64_t)fpg * p.page_stride + fh * kHeadDim;
       const int64_t lane_off = (lane & 15) * p.tok_stride + 8 * (lane >> 4);
@@ -494,10 +521,14 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
     const int nbt_hi = io.bt_hi;
 
     if (claiming) zi = 2 * W + C * __builtin_amdgcn_readfirstlane(craw) + jc;
+    if (listed && taking) {
+      zi = nx < nx_end ? nx : N;
+      ++nx;
+    }
     // Z's descriptor is needed now only when this is X's last page and Y is
     // a single page (Z's first page is then the next DMA); otherwise it is
     // fetched after the compute below.
-    const bool z_now = claiming && zi < N && i + 1 == np && Y[2] - Y[1] == 1;
+    const bool z_now = taking && zi < N && i + 1 == np && Y[2] - Y[1] == 1;
     if (z_now) {
       Z = desc_at(zi);
       z_len = sload(p.seq_lens, Z[0]);
@@ -532,7 +563,7 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
     // Z's descriptor and length, fetched after this page's LDS reads so the
     // scalar loads overlap the next page's wait.
     __builtin_amdgcn_sched_barrier(0);
-    if (claiming && zi < N && !z_now) {
+    if (taking && zi < N && !z_now) {
       Z = desc_at(zi);
       z_len = sload(p.seq_lens, Z[0]);
     }
@@ -563,8 +594,9 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
   // Count this wavefront out; the last one resets the scheduler for the next
   // launch.  Every claim this wavefront made has returned by now (each was
   // retired by the wait of the iteration that issued it), so all claims
-  // precede the reset.
+  // precede the reset.  Piece lists touch no counter.
   __builtin_amdgcn_s_waitcnt(kVmcnt0);
+  if (listed) return;
   int* const exit_ctr = p.sched + kDecodeClaimCounters * kDecodeSchedLineInts;
   int gone = 0;
   if (lane == 0) gone = __hip_atomic_fetch_add(exit_ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -6,10 +6,29 @@
 namespace mva {
 namespace {
 
+// kWaves wavefronts per workgroup, each with private LDS buffers; wavefront
+// w of workgroup b is decode wavefront b * kWaves + w.
+template <typename T, int kWaves>
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_kernel(
+    DecodeParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kWaves * kDecodeWaveLdsBytes];
+  const int w = kWaves == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int wave = (int)blockIdx.x * kWaves + w;
+  if (wave >= p.num_waves) return;
+  decode_wave<T>(p, wave, (lds_u8*)lds + w * kDecodeWaveLdsBytes);
+}
+
 template <typename T>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_kernel(DecodeParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kDecodeWaveLdsBytes];
-  decode_wave<T>(p, (int)blockIdx.x, (lds_u8*)lds);
+int launch_paged_decode(const DecodeParams& p, int waves_per_group, hipStream_t s) {
+  const uint32_t blocks = (uint32_t)((p.num_waves + waves_per_group - 1) / waves_per_group);
+  switch (waves_per_group) {
+    case 1: hipLaunchKernelGGL((paged_decode_kernel<T, 1>), dim3(blocks), dim3(64), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((paged_decode_kernel<T, 2>), dim3(blocks), dim3(128), 0, s, p); break;
+    case 4: hipLaunchKernelGGL((paged_decode_kernel<T, 4>), dim3(blocks), dim3(256), 0, s, p); break;
+    case 8: hipLaunchKernelGGL((paged_decode_kernel<T, 8>), dim3(blocks), dim3(512), 0, s, p); break;
+    default: return set_error("paged attention: waves_per_group must be 1, 2, 4 or 8");
+  }
+  return check_launch("paged_decode");
 }
 
 // Split-K merges: four wavefronts per workgroup, one per (merge entry,
@@ -51,7 +70,7 @@ int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, i
                        const void* k_cache, const void* v_cache, int64_t num_pages, int64_t page_stride,
                        int64_t token_stride, const int32_t* block_tables, int64_t block_table_stride,
                        const int32_t* seq_lens, const int32_t* items, int64_t num_items, int64_t num_waves,
-                       const int32_t* merges, int64_t num_merges, int64_t num_part_slots, void* out,
+                       const int32_t* wave_extra, const int32_t* merges, int64_t num_merges, int64_t num_part_slots, void* out,
                        int64_t out_token_stride,
                        int64_t out_head_stride, void* workspace, int64_t workspace_bytes,
                        int num_q_heads, int num_kv_heads, int head_dim, int page_size,
@@ -94,6 +113,7 @@ int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, i
   p.items = items;
   p.num_items = (int)num_items;
   p.num_waves = (int)num_waves;
+  p.wave_extra = wave_extra;
   p.out = out;
   p.out_tok_stride = out_token_stride;
   p.out_head_stride = out_head_stride;
@@ -121,6 +141,7 @@ extern "C" int mva_paged_decode(const void* q, int64_t q_token_stride, int64_t q
                                 int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
                                 int64_t block_table_stride, const int32_t* seq_lens,
                                 const int32_t* items, int64_t num_items, int64_t num_waves,
+                                const int32_t* wave_extra, int waves_per_group,
                                 const int32_t* merges, int64_t num_merges,
                                 int64_t num_part_slots, void* out, int64_t out_token_stride,
                                 int64_t out_head_stride, void* workspace, int64_t workspace_bytes,
@@ -130,18 +151,18 @@ extern "C" int mva_paged_decode(const void* q, int64_t q_token_stride, int64_t q
   DecodeParams p;
   int rc = fill_decode_params(p, q, q_token_stride, q_head_stride, k_cache, v_cache, num_pages,
                               page_stride, token_stride, block_tables, block_table_stride, seq_lens,
-                              items, num_items, num_waves, merges, num_merges, num_part_slots, out,
+                              items, num_items, num_waves, wave_extra, merges, num_merges, num_part_slots, out,
                               out_token_stride,
                               out_head_stride, workspace, workspace_bytes, num_q_heads, num_kv_heads,
                               head_dim, page_size, softmax_scale);
   if (rc) return rc;
+  if (wave_extra == nullptr && waves_per_group != 1)
+    return set_error("paged attention: the claim schedule runs one wavefront per workgroup");
   if (num_items == 0) return 0;
-  const dim3 grid((uint32_t)num_waves);
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == kBF16) hipLaunchKernelGGL(paged_decode_kernel<__bf16>, grid, dim3(64), 0, s, p);
-  else if (dtype == kF16) hipLaunchKernelGGL(paged_decode_kernel<_Float16>, grid, dim3(64), 0, s, p);
+  if (dtype == kBF16) rc = launch_paged_decode<__bf16>(p, waves_per_group, s);
+  else if (dtype == kF16) rc = launch_paged_decode<_Float16>(p, waves_per_group, s);
   else return set_error("paged attention: dtype must be bf16 or fp16");
-  rc = check_launch("paged_decode");
   if (rc) return rc;
   return launch_decode_merge(p, merges, num_merges, dtype, s);
 }

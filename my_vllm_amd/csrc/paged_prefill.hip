@@ -9,7 +9,7 @@ int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, i
                        const void* k_cache, const void* v_cache, int64_t num_pages, int64_t page_stride,
                        int64_t token_stride, const int32_t* block_tables, int64_t block_table_stride,
                        const int32_t* seq_lens, const int32_t* items, int64_t num_items, int64_t num_waves,
-                       const int32_t* merges, int64_t num_merges, int64_t num_part_slots, void* out,
+                       const int32_t* wave_extra, const int32_t* merges, int64_t num_merges, int64_t num_part_slots, void* out,
                        int64_t out_token_stride,
                        int64_t out_head_stride, void* workspace, int64_t workspace_bytes,
                        int num_q_heads, int num_kv_heads, int head_dim, int page_size,
@@ -180,7 +180,8 @@ extern "C" int mva_paged_mixed(const void* q, int64_t q_token_stride, int64_t q_
   DecodeParams dp;
   rc = fill_decode_params(dp, q, q_token_stride, q_head_stride, k_cache, v_cache, num_pages, page_stride,
                           token_stride, block_tables, block_table_stride, seq_lens, decode_items,
-                          num_decode_items, num_decode_waves, decode_merges, num_decode_merges, num_part_slots, out,
+                          num_decode_items, num_decode_waves, nullptr, decode_merges, num_decode_merges, num_part_slots,
+                          out,
                           out_token_stride, out_head_stride,
                           workspace, workspace_bytes, num_q_heads, num_kv_heads, head_dim, page_size,
                           softmax_scale);

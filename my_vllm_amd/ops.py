@@ -154,12 +154,17 @@ def paged_decode(
     out: torch.Tensor,
     workspace: torch.Tensor | None,
     softmax_scale: float,
+    wave_extra: torch.Tensor | None = None,
+    waves_per_group: int = 1,
 ) -> None:
     """Launch the paged GQA decode kernel over prepared pieces.
 
     ``q``/``out`` are ``[T, Hq, D]`` views (rows addressed by the pieces'
     ``q_row``); caches ``[P, page, Hkv, D]``; ``items`` int32 ``[n, 8]``,
-    claimed by ``num_waves`` (``1 <= num_waves <= n``) wavefronts;
+    run by ``num_waves`` (``1 <= num_waves <= n``) wavefronts, ``waves_per_group``
+    to a workgroup.  With ``wave_extra`` (int32 ``[num_waves + 1]``) wavefront
+    ``w`` runs piece ``w`` and then pieces ``wave_extra[w]:wave_extra[w + 1]``;
+    without it, wavefronts claim pieces from workspace counters.
     ``merges`` (see :func:`decode_merge_list`) lists the split segments whose
     partials the follow-up merge kernel combines.
     """
@@ -173,6 +178,7 @@ def paged_decode(
         k_cache.data_ptr(), v_cache.data_ptr(), num_pages, k_cache.stride(0), k_cache.stride(1),
         block_tables.data_ptr(), block_tables.stride(0), seq_lens.data_ptr(),
         items.data_ptr(), num_items, num_waves,
+        wave_extra.data_ptr() if wave_extra is not None else 0, int(waves_per_group),
         merges.data_ptr() if merges is not None else 0, num_merges, num_part_slots,
         out.data_ptr(), out.stride(0), out.stride(1),
         ws_ptr, ws_bytes,

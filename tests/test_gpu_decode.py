@@ -19,6 +19,7 @@ from my_vllm_amd.attention_backend import (
     MI355XAttentionBackend,
     _to_device,
     make_decode_plan,
+    make_decode_plan_listed,
 )
 from my_vllm_amd.context import BatchType
 from my_vllm_amd.workloads import config_decode_small, decode_lengths, make_paged_batch
@@ -61,9 +62,12 @@ def test_reference_shapes(gpu):
     assert_attention_close(out, _expected(batch))
 
 
-def test_qwen3_0p6b_decode_configuration(gpu):
+@pytest.mark.parametrize("schedule", ["listed", "claims"])
+def test_qwen3_0p6b_decode_configuration(gpu, monkeypatch, schedule):
+    monkeypatch.setenv("MVA_DECODE_SCHEDULE", schedule)
     batch = config_decode_small(seed=1)
-    out, *_ = _run(batch, gpu)
+    out, backend, plan, _ = _run(batch, gpu)
+    assert (plan.metadata.decode_wave_extra is not None) == (schedule == "listed")
     assert_attention_close(out, _expected(batch))
 
 
@@ -75,12 +79,15 @@ def test_gqa_ratios(gpu, hq, hkv):
     assert_attention_close(out, _expected(batch))
 
 
+@pytest.mark.parametrize("schedule", ["listed", "claims"])
 @pytest.mark.parametrize("waves", [1, 7, 64, 2048, 100000])
-def test_split_k_merge(gpu, monkeypatch, waves):
-    # The piece length follows the wave count: 1 wave claims every piece
-    # (128-page pieces) itself; 100000 waves give 4-page pieces and one
-    # wavefront per piece.
+def test_split_k_merge(gpu, monkeypatch, waves, schedule):
+    # Claims: the piece length follows the wave count: 1 wave claims every
+    # piece (128-page pieces) itself; 100000 waves give 4-page pieces and one
+    # wavefront per piece.  Piece lists: waves / 8 page ranges (at least
+    # one), down to one page per range.
     monkeypatch.setenv("MVA_DECODE_WAVES", str(waves))
+    monkeypatch.setenv("MVA_DECODE_SCHEDULE", schedule)
     ctx = [1, 16, 17, 255, 256, 257, 1000, 3001, 4096, 2049]
     batch = make_paged_batch(43, [1] * len(ctx), ctx, 0, 32, 8)
     out, backend, plan, args = _run(batch, gpu)
@@ -118,6 +125,46 @@ def test_piece_plans_through_c_abi(gpu, waves, per_wave, min_pages):
     ops.paged_decode(*args)
     assert torch.equal(out, first)
     assert int(ws[:8].view(torch.int32).abs().sum().item()) == 0
+
+
+@pytest.mark.parametrize(
+    "hq,hkv,groups,max_piece",
+    [(32, 8, 1, 128), (32, 8, 7, 3), (32, 8, 256, 128), (16, 4, 100, 1), (8, 2, 33, 5), (8, 1, 13, 128),
+     (12, 3, 50, 2), (16, 8, 100000, 128), (128, 8, 40, 7)],
+)
+def test_piece_lists_through_c_abi(gpu, hq, hkv, groups, max_piece):
+    # Equal page ranges per workgroup (one wavefront per KV head when the
+    # head count divides 8), one-page and 3-page pieces, ranges of one page,
+    # one range over the whole batch; a second launch must be identical and
+    # leave the claim counters untouched.
+    ctx = [1, 16, 17, 40, 1, 300, 33, 2049, 5, 640]
+    batch = make_paged_batch(71, [1] * len(ctx), ctx, 0, hq, hkv)
+    common, q, kc, vc = _to(batch, gpu)
+    counts = np.asarray([(n + 15) // 16 for n in ctx])
+    items, wave_extra, nw, slots = make_decode_plan_listed(counts, 0, 0, hkv, groups, max_piece)
+    per_group = hkv if hkv in (1, 2, 4, 8) else 1
+    ws = torch.zeros(ops.decode_workspace_bytes(slots, hkv, hq // hkv), dtype=torch.uint8, device=gpu)
+    out = torch.full_like(q, float("nan"))
+    merges = ops.decode_merge_list(items)
+    args = (q, kc, vc, common.block_tables, common.seq_lens, _to_device(items, gpu), items.shape[0], nw,
+            _to_device(merges, gpu) if len(merges) else None, merges.shape[0], slots, out, ws, 128 ** -0.5)
+    extra = _to_device(wave_extra, gpu)
+    ops.paged_decode(*args, wave_extra=extra, waves_per_group=per_group)
+    first = out.clone()
+    assert_attention_close(first, _expected(batch))
+    ops.paged_decode(*args, wave_extra=extra, waves_per_group=per_group)
+    assert torch.equal(out, first)
+    assert int(ws[:4352].view(torch.int32).abs().sum().item()) == 0
+
+
+def test_claim_schedule_rejects_multi_wave_groups(gpu):
+    batch = make_paged_batch(73, [1, 1], [40, 7], 0, 16, 8)
+    common, q, kc, vc = _to(batch, gpu)
+    items, nw, slots = make_decode_plan(np.asarray([3, 1]), 0, 0, 8, 64)
+    ws = torch.zeros(ops.decode_workspace_bytes(slots, 8, 2), dtype=torch.uint8, device=gpu)
+    with pytest.raises(RuntimeError, match="one wavefront per workgroup"):
+        ops.paged_decode(q, kc, vc, common.block_tables, common.seq_lens, _to_device(items, gpu), items.shape[0],
+                         nw, None, 0, slots, torch.empty_like(q), ws, 128 ** -0.5, waves_per_group=8)
 
 
 @pytest.mark.parametrize("hq,hkv", [(8, 8), (24, 8), (40, 8), (128, 8)])

@@ -23,6 +23,7 @@ from my_vllm_amd.attention_backend import (
     MI355XAttentionMetadata,
     MI355XSplitAttentionBackend,
     make_decode_plan,
+    make_decode_plan_listed,
     make_prefill_items,
 )
 from my_vllm_amd.context import BatchType, CommonAttentionMetadata
@@ -241,6 +242,69 @@ def test_decode_plan_edges():
     assert empty.shape == (0, ops.DECODE_ITEM_INTS) and nw == 0 and slots == 0
     with pytest.raises(ValueError):
         make_decode_plan(np.array([0]), 0, 0, 8, 2048)
+
+
+def _check_listed_plan(counts, hkv, groups, max_piece):
+    counts = np.asarray(counts, dtype=np.int64)
+    items, wave_extra, nw, slots = make_decode_plan_listed(counts, 3, 7, hkv, groups, max_piece)
+    total = int(counts.sum())
+    g = min(groups, total)
+    offsets = np.concatenate(([0], np.cumsum(counts)))
+    assert items.dtype == np.int32 and items.shape[1] == ops.DECODE_ITEM_INTS
+    assert nw == g * hkv and wave_extra.dtype == np.int32 and wave_extra.shape == (nw + 1,)
+    assert wave_extra[0] == nw and wave_extra[-1] == len(items) and np.all(np.diff(wave_extra) >= 0)
+    covered = np.zeros((hkv, total), dtype=np.int64)
+    slot_ids = set()
+    segments = {}
+    for w in range(nw):
+        rows = [w] + list(range(wave_extra[w], wave_extra[w + 1]))
+        spans = []
+        for r in rows:
+            s, pb, pe, ch, nc, base, qrow, h = (int(x) for x in items[r])
+            i = s - 3
+            assert qrow == 7 + i and h == w % hkv and 0 <= pb < pe <= counts[i] and pe - pb <= max_piece
+            spans.append((offsets[i] + pb, offsets[i] + pe))
+            covered[h, offsets[i] + pb:offsets[i] + pe] += 1
+            segments.setdefault((i, h), []).append((pb, pe, ch, nc, base))
+            if nc > 1:
+                slot = (base + ch) * hkv + h
+                assert slot not in slot_ids and base + ch < slots
+                slot_ids.add(slot)
+        # The wavefront's pieces tile its range [r*T//g, (r+1)*T//g) in page order.
+        r = w // hkv
+        assert spans[0][0] == r * total // g and spans[-1][1] == (r + 1) * total // g
+        assert all(a[1] == b[0] for a, b in zip(spans, spans[1:]))
+    assert np.all(covered == 1), "every (page, KV head) exactly once"
+    for (i, h), pieces in segments.items():
+        nc = pieces[0][3]
+        assert [p[2] for p in pieces] == list(range(nc)) and {p[3] for p in pieces} == {nc}
+        assert pieces[0][0] == 0 and pieces[-1][1] == counts[i]
+    pages = np.diff((np.arange(g + 1) * total) // g)
+    assert pages.max() - pages.min() <= 1, "equal share per wavefront"
+    return items, wave_extra, nw, slots
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_listed_decode_plan_tiles_every_wavefront_range(seed):
+    rng = np.random.default_rng(500 + seed)
+    counts = rng.integers(1, 400, size=int(rng.integers(1, 40))).tolist()
+    _check_listed_plan(counts, int(rng.choice([1, 2, 3, 4, 8])), int(rng.integers(1, 3000)),
+                       int(rng.choice([1, 3, 17, 128])))
+
+
+def test_listed_decode_plan_edges():
+    items, wave_extra, nw, slots = _check_listed_plan([1], 8, 256, 128)
+    assert nw == 8 and len(items) == 8 and slots == 0 and wave_extra.tolist() == [8] * 9
+    # More workgroups than pages: one page per range.
+    items, _, nw, _ = _check_listed_plan([3, 2], 4, 1000, 128)
+    assert nw == 5 * 4
+    # One range over a long sequence: pieces of at most 128 pages, chunked.
+    items, _, nw, slots = _check_listed_plan([300], 2, 1, 128)
+    assert nw == 2 and slots == 3
+    empty, wave_extra, nw, slots = make_decode_plan_listed(np.zeros(0, np.int64), 0, 0, 8, 256)
+    assert empty.shape == (0, ops.DECODE_ITEM_INTS) and nw == 0 and slots == 0
+    with pytest.raises(ValueError):
+        make_decode_plan_listed(np.array([0]), 0, 0, 8, 256)
 
 
 @pytest.mark.parametrize("seed", range(10))

@@ -35,7 +35,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     lib = _native.load_library()
     for name in _declared_functions():
         assert hasattr(lib, name), f"{name} missing from {_native.LIB_PATH.name}"
-    assert lib.mva_abi_version() == 2
+    assert lib.mva_abi_version() == 3
 
 
 def test_library_binds_to_the_process_hip_runtime():
@@ -65,7 +65,7 @@ def test_invalid_arguments_fail_before_launch_with_a_message():
     assert lib.mva_last_error().decode()
     # head_dim 64 is rejected by the decode entry point before anything runs.
     with pytest.raises(RuntimeError, match="mva_paged_decode failed"):
-        _native.call("mva_paged_decode", 0, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0, 1, 1, 0, 0, 0, 0, 0, 0, 0, 0,
+        _native.call("mva_paged_decode", 0, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0, 1, 1, 0, 1, 0, 0, 0, 0, 0, 0, 0, 0,
                      16, 8, 64, 16, 1.0, 0, 0)
 
 
