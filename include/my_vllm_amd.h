@@ -118,6 +118,39 @@ int mva_paged_decode(const void* q, int64_t q_token_stride, int64_t q_head_strid
                      int64_t workspace_bytes, int num_q_heads, int num_kv_heads, int head_dim,
                      int page_size, float softmax_scale, int dtype, void* stream);
 
+/*
+ * Fixed-shape variant of mva_paged_decode for capture in a HIP graph: every
+ * argument that changes from one decode step to the next lives in device
+ * memory at a fixed address, so one captured launch serves every step whose
+ * plan fits the capacities.
+ *   counts [3] int32 (device): {num_items, num_waves, num_merges} of this
+ *         step, each clamped to its capacity; wavefronts and merge
+ *         wavefronts past them exit at once.
+ *   items  [item_capacity, 8], wave_extra [wave_capacity + 1], merges
+ *         [merge_capacity, 8]: the piece-list schedule of mva_paged_decode
+ *         (wave_extra is required; no claims).
+ *   wave_capacity (<= item_capacity) wavefronts and merge_capacity x
+ *         (num_q_heads / num_kv_heads) merge wavefronts are launched.
+ *   num_part_slots: split-K partial slots the largest fitting plan uses
+ *         (sizes the workspace).
+ * Other arguments as mva_paged_decode; block_tables, seq_lens, q, out and
+ * the workspace must also stay at fixed addresses while a graph holds the
+ * launch.  No counter in the workspace is used.
+ * Serves the reference's full-decode CUDA-graph hooks
+ * (nanovllm/layers/attention_backend.py:242-275, FlashInfer version
+ * :1028-1225; capture and replay in nanovllm/engine/model_runner.py:631-742).
+ */
+int mva_paged_decode_graph(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                           const void* k_cache, const void* v_cache, int64_t num_pages,
+                           int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
+                           int64_t block_table_stride, const int32_t* seq_lens, const int32_t* counts,
+                           const int32_t* items, int64_t item_capacity, const int32_t* wave_extra,
+                           int64_t wave_capacity, int waves_per_group, const int32_t* merges,
+                           int64_t merge_capacity, int64_t num_part_slots, void* out,
+                           int64_t out_token_stride, int64_t out_head_stride, void* workspace,
+                           int64_t workspace_bytes, int num_q_heads, int num_kv_heads, int head_dim,
+                           int page_size, float softmax_scale, int dtype, void* stream);
+
 /* Query-token rows per prefill workgroup tile for a GQA ratio (128 / ratio),
  * or -1 for invalid head counts. */
 int mva_prefill_tile_tokens(int num_q_heads, int num_kv_heads);

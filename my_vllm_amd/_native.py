@@ -47,6 +47,20 @@ _SIGNATURES = {
             _i32, _i32, _i32, _i32, _f32, _i32, _c_void_p,  # heads, head_dim, page, scale, dtype, stream
         ],
     ),
+    "mva_paged_decode_graph": (
+        _i32,
+        [
+            _c_void_p, _i64, _i64,  # q, q_token_stride, q_head_stride
+            _c_void_p, _c_void_p, _i64, _i64, _i64,  # k_cache, v_cache, num_pages, page_stride, token_stride
+            _c_void_p, _i64, _c_void_p,  # block_tables, block_table_stride, seq_lens
+            _c_void_p,  # counts
+            _c_void_p, _i64, _c_void_p, _i64, _i32,  # items, item_capacity, wave_extra, wave_capacity, waves_per_group
+            _c_void_p, _i64, _i64,  # merges, merge_capacity, num_part_slots
+            _c_void_p, _i64, _i64,  # out, out_token_stride, out_head_stride
+            _c_void_p, _i64,  # workspace, workspace_bytes
+            _i32, _i32, _i32, _i32, _f32, _i32, _c_void_p,
+        ],
+    ),
     "mva_prefill_tile_tokens": (_i32, [_i32, _i32]),
     "mva_paged_prefill": (
         _i32,

@@ -293,6 +293,8 @@ class MI355XAttentionMetadata:
     num_decode_merges: int = 0
     decode_wave_extra: torch.Tensor | None = None
     decode_waves_per_group: int = 1
+    # Host copy of a piece-list plan: (items, wave_extra, merges, workgroups).
+    decode_host_plan: tuple | None = None
     prefill_items: torch.Tensor | None = None
     num_prefill_items: int = 0
 
@@ -542,6 +544,86 @@ def _device_arch(device: torch.device) -> str:
     return getattr(props, "gcnArchName", "") or ""
 
 
+@dataclass
+class MI355XFullDecodeGraphState:
+    """Fixed-address buffers of one captured full-decode graph (one batch size).
+
+    ``plan_buffer`` holds ``{num_items, num_waves, num_merges}``, then the
+    pieces (``item_capacity`` x 8), the piece-list offsets (``wave_capacity``
+    + 1) and the merge list (``merge_capacity`` x 8), as laid out by
+    :func:`pack_graph_decode_plan`.  Mirrors the reference's
+    ``_FlashInferFullDecodeGraphState`` (attention_backend.py:162-171).
+    """
+
+    batch_size: int
+    page_indices_capacity: int
+    groups: int
+    waves_per_group: int
+    item_capacity: int
+    wave_capacity: int
+    merge_capacity: int
+    part_slot_capacity: int
+    block_tables_buffer: torch.Tensor
+    seq_lens_buffer: torch.Tensor
+    plan_buffer: torch.Tensor
+    plan_staging: torch.Tensor
+    staging_ready: Any
+    workspace: torch.Tensor
+    output: torch.Tensor
+    plan: Any = None
+
+    def views(self):
+        """(counts, items, wave_extra, merges) views of the device plan buffer."""
+        return split_graph_plan_buffer(self.plan_buffer, self.item_capacity, self.wave_capacity,
+                                       self.merge_capacity)
+
+
+def graph_decode_capacities(batch_size: int, page_capacity: int, num_kv_heads: int, groups: int) -> dict:
+    """Largest piece-list plan of ``batch_size`` sequences over at most
+    ``page_capacity`` pages (``make_decode_plan_listed`` with ``groups``
+    workgroups): the page ranges and sequences cut the pages into at most
+    ``groups + batch_size - 1`` intervals, each split into ``ceil(L/128)``
+    pieces per KV head."""
+    intervals = groups + batch_size + page_capacity // ops.MAX_CHUNK_PAGES + 1
+    return {
+        "item_capacity": intervals * num_kv_heads,
+        "wave_capacity": groups * num_kv_heads,
+        "merge_capacity": batch_size * num_kv_heads,
+        "part_slot_capacity": intervals,
+    }
+
+
+def graph_plan_buffer_ints(item_capacity: int, wave_capacity: int, merge_capacity: int) -> int:
+    return 3 + item_capacity * ops.DECODE_ITEM_INTS + wave_capacity + 1 + merge_capacity * ops.DECODE_ITEM_INTS
+
+
+def split_graph_plan_buffer(buffer, item_capacity: int, wave_capacity: int, merge_capacity: int):
+    """(counts, items, wave_extra, merges) views of a packed graph plan."""
+    a = 3
+    b = a + item_capacity * ops.DECODE_ITEM_INTS
+    c = b + wave_capacity + 1
+    d = c + merge_capacity * ops.DECODE_ITEM_INTS
+    return (buffer[:a], buffer[a:b].reshape(item_capacity, ops.DECODE_ITEM_INTS), buffer[b:c],
+            buffer[c:d].reshape(merge_capacity, ops.DECODE_ITEM_INTS))
+
+
+def pack_graph_decode_plan(items: np.ndarray, wave_extra: np.ndarray, merges: np.ndarray, item_capacity: int,
+                           wave_capacity: int, merge_capacity: int, out: np.ndarray | None = None) -> np.ndarray:
+    """Lay a piece-list plan out at the fixed offsets of a graph plan buffer."""
+    waves = wave_extra.size - 1
+    if items.shape[0] > item_capacity or waves > wave_capacity or merges.shape[0] > merge_capacity:
+        raise ValueError("decode plan exceeds the graph state's capacity")
+    size = graph_plan_buffer_ints(item_capacity, wave_capacity, merge_capacity)
+    if out is None:
+        out = np.zeros(size, dtype=np.int32)
+    counts, it, we, mg = split_graph_plan_buffer(out, item_capacity, wave_capacity, merge_capacity)
+    counts[:] = (items.shape[0], waves, merges.shape[0])
+    it[: items.shape[0]] = items
+    we[: waves + 1] = wave_extra
+    mg[: merges.shape[0]] = merges
+    return out
+
+
 class MI355XAttentionBackendMixin:
     """The MI355X backend implementation, independent of the concrete base class.
 
@@ -550,7 +632,7 @@ class MI355XAttentionBackendMixin:
     """
 
     backend_name = "mi355x"
-    supports_full_decode_graph = False
+    supports_full_decode_graph = True
     default_attention_mode = "unified"
     plan_type: type = AttentionPlan
     route_type: type = AttentionRoute
@@ -590,6 +672,7 @@ class MI355XAttentionBackendMixin:
         self._route_counts = {route.value: 0 for route in self.route_type}
         self._output_buffer: torch.Tensor | None = None
         self._workspace: torch.Tensor | None = None
+        self._active_graph_state: MI355XFullDecodeGraphState | None = None
 
     # ---- capability contract -------------------------------------------------
     @classmethod
@@ -687,6 +770,7 @@ class MI355XAttentionBackendMixin:
         decode_items = None
         decode_merges = None
         decode_wave_extra = None
+        decode_host_plan = None
         num_decode_items = 0
         num_decode_merges = 0
         num_decode_waves = 0
@@ -724,6 +808,7 @@ class MI355XAttentionBackendMixin:
             decode_merges = flat[n_items:n_items + n_merge].view(num_decode_merges, ops.DECODE_ITEM_INTS)
             if wave_extra is not None:
                 decode_wave_extra = flat[n_items + n_merge:]
+                decode_host_plan = (items, wave_extra, merges, groups)
         prefill_items = None
         num_prefill_items = 0
         if common.num_prefill_seqs:
@@ -759,6 +844,7 @@ class MI355XAttentionBackendMixin:
             num_decode_merges=num_decode_merges,
             decode_wave_extra=decode_wave_extra,
             decode_waves_per_group=waves_per_group,
+            decode_host_plan=decode_host_plan,
             prefill_items=prefill_items,
             num_prefill_items=num_prefill_items,
         )
@@ -839,6 +925,15 @@ class MI355XAttentionBackendMixin:
         has_v_cache = _has_cache(v_cache)
         if has_k_cache != has_v_cache:
             raise ValueError("key and value caches must both be present or absent")
+        graph_state = self._active_graph_state
+        if graph_state is not None:
+            if not has_k_cache:
+                raise RuntimeError("full decode graph requires allocated KV cache")
+            self._validate_inputs(q, k_cache, v_cache)
+            if graph_state.output.shape != q.shape:
+                raise RuntimeError("decode graph attention output does not match query shape")
+            self._run_decode_graph(q, k_cache, v_cache, graph_state)
+            return graph_state.output
         route = plan.route
         if route is Route.WARMUP:
             if has_k_cache:
@@ -907,6 +1002,119 @@ class MI355XAttentionBackendMixin:
             metadata.decode_wave_extra,
             metadata.decode_waves_per_group,
         )
+
+    def _run_decode_graph(self, q, k_cache, v_cache, state: MI355XFullDecodeGraphState) -> None:
+        counts, items, wave_extra, merges = state.views()
+        ops.paged_decode_graph(
+            q, k_cache, v_cache, state.block_tables_buffer, state.seq_lens_buffer, counts, items, wave_extra,
+            state.waves_per_group, merges, state.part_slot_capacity, state.output, state.workspace,
+            self.softmax_scale,
+        )
+
+    # ---- full-decode HIP graph (reference attention_backend.py:242-275, 1028-1225) ----
+    def create_full_decode_graph_state(self, batch_size: int, page_indices_capacity: int, device):
+        if isinstance(batch_size, bool) or not isinstance(batch_size, int):
+            raise TypeError("batch_size must be an int")
+        if isinstance(page_indices_capacity, bool) or not isinstance(page_indices_capacity, int):
+            raise TypeError("page_indices_capacity must be an int")
+        if batch_size <= 0 or page_indices_capacity < batch_size:
+            raise ValueError("graph state requires positive batch and page capacity")
+        graph_device = torch.device(device)
+        if graph_device.type != "cuda":
+            raise ValueError("full decode graph state must be on CUDA")
+        groups, waves_per_group = listed_decode_groups(self.num_kv_heads, graph_device)
+        caps = graph_decode_capacities(batch_size, page_indices_capacity, self.num_kv_heads, groups)
+        group = self.num_q_heads // self.num_kv_heads
+        plan_ints = graph_plan_buffer_ints(caps["item_capacity"], caps["wave_capacity"], caps["merge_capacity"])
+        ws_bytes = ops.decode_workspace_bytes(caps["part_slot_capacity"], self.num_kv_heads, group)
+        width = max(1, page_indices_capacity // batch_size)
+        return MI355XFullDecodeGraphState(
+            batch_size=batch_size,
+            page_indices_capacity=page_indices_capacity,
+            groups=groups,
+            waves_per_group=waves_per_group,
+            block_tables_buffer=torch.zeros((batch_size, width), dtype=torch.int32, device=graph_device),
+            seq_lens_buffer=torch.ones(batch_size, dtype=torch.int32, device=graph_device),
+            plan_buffer=torch.zeros(plan_ints, dtype=torch.int32, device=graph_device),
+            plan_staging=torch.zeros(plan_ints, dtype=torch.int32, pin_memory=True),
+            staging_ready=None,
+            workspace=torch.zeros(ws_bytes, dtype=torch.uint8, device=graph_device),
+            output=torch.empty(batch_size, self.num_q_heads, self.head_dim, dtype=self.dtype, device=graph_device),
+            **caps,
+        )
+
+    def full_decode_graph_metadata_fits(self, state, plan) -> bool:
+        if not isinstance(state, MI355XFullDecodeGraphState) or not isinstance(plan, self.plan_type):
+            return False
+        if plan.batch_type is not self.batch_type_enum.PURE_DECODE or plan.route is not self.route_type.DECODE:
+            return False
+        metadata = plan.metadata
+        if not isinstance(metadata, MI355XAttentionMetadata) or metadata.is_cacheless:
+            return False
+        common = plan.common
+        if common.num_prefill_seqs != 0 or common.num_prefill_tokens != 0:
+            return False
+        if common.num_decode_seqs != state.batch_size or common.num_decode_tokens != state.batch_size:
+            return False
+        bt = metadata.block_tables
+        if (
+            not isinstance(bt, torch.Tensor)
+            or bt.dtype != torch.int32
+            or bt.device.type != "cuda"
+            or bt.ndim != 2
+            or bt.size(0) != state.batch_size
+            or bt.size(1) > state.block_tables_buffer.size(1)
+        ):
+            return False
+        if metadata.num_pages > state.page_indices_capacity or metadata.num_prefill_pages != 0:
+            return False
+        for tensor in (metadata.seq_lens, common.slot_mapping):
+            if (
+                not isinstance(tensor, torch.Tensor)
+                or tensor.dtype != torch.int32
+                or tensor.device.type != "cuda"
+                or tensor.ndim != 1
+                or tensor.numel() != state.batch_size
+            ):
+                return False
+        return True
+
+    def plan_full_decode_graph(self, state, plan) -> None:
+        if not self.full_decode_graph_metadata_fits(state, plan):
+            raise ValueError("attention plan does not fit full decode graph state")
+        metadata = plan.metadata
+        host = metadata.decode_host_plan
+        if host is None or host[3] != state.groups:
+            counts = np.diff(np.asarray(metadata.kv_indptr, dtype=np.int64))
+            items, wave_extra, _, _ = make_decode_plan_listed(counts, 0, 0, self.num_kv_heads, state.groups)
+            merges = ops.decode_merge_list(items)
+        else:
+            items, wave_extra, merges, _ = host
+        # The previous step's copy must have read the staging buffer first.
+        if state.staging_ready is not None:
+            state.staging_ready.synchronize()
+        pack_graph_decode_plan(items, wave_extra, merges, state.item_capacity, state.wave_capacity,
+                               state.merge_capacity, state.plan_staging.numpy())
+        state.plan_buffer.copy_(state.plan_staging, non_blocking=True)
+        event = torch.cuda.Event()
+        event.record()
+        state.staging_ready = event
+        bt = metadata.block_tables
+        state.block_tables_buffer[:, : bt.size(1)].copy_(bt)
+        state.seq_lens_buffer.copy_(metadata.seq_lens)
+        state.plan = plan
+
+    def activate_full_decode_graph(self, state) -> None:
+        if not isinstance(state, MI355XFullDecodeGraphState):
+            raise TypeError("invalid MI355X decode graph state")
+        if state.plan is None:
+            raise RuntimeError("decode graph state must be planned before activation")
+        if self._active_graph_state is not None:
+            raise RuntimeError("a decode graph state is already active")
+        self._active_graph_state = state
+
+    def deactivate_full_decode_graph(self) -> None:
+        self._active_graph_state = None
 
     def _run_prefill(self, q, k_cache, v_cache, common, metadata: MI355XAttentionMetadata, output) -> None:
         ops.paged_prefill(

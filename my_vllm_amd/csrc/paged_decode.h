@@ -87,6 +87,10 @@ struct DecodeParams {
   // Piece lists: wavefront w runs piece w, then pieces
   // [wave_extra[w], wave_extra[w + 1]).  nullptr: the claim schedule.
   const int32_t* wave_extra;
+  // Fixed-shape (graph) launches: {num_items, num_waves, num_merges} read on
+  // the device, each clamped to the launch's capacity (num_items, num_waves
+  // and the merge grid then hold capacities).  nullptr: the scalars above.
+  const int32_t* counts;
   int32_t* sched;  // claim counters and exit counter, see kDecodeClaimCounters
   void* out;
   int64_t out_tok_stride;
@@ -286,8 +290,10 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
   const int c = lane & 15;
   const int G = p.group;
   const int Hkv = p.num_kv_heads;
-  const int W = p.num_waves;
-  const int N = p.num_items;
+  // Graph launches read this step's counts; wavefronts past them have no work.
+  const int W = p.counts ? min(sload(p.counts, 1), p.num_waves) : p.num_waves;
+  const int N = p.counts ? min(sload(p.counts, 0), p.num_items) : p.num_items;
+  if (wave >= W || wave >= N) return;
   const int C = min(kDecodeClaimCounters, max(1, W >> 3));
   const int jc = (wave >> 3) % C;
   const bool q_lane = c < G;

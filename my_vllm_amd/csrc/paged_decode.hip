@@ -32,12 +32,14 @@ int launch_paged_decode(const DecodeParams& p, int waves_per_group, hipStream_t 
 }
 
 // Split-K merges: four wavefronts per workgroup, one per (merge entry,
-// query head).
+// query head).  Graph launches size the grid for the merge capacity and read
+// this step's merge count from p.counts[2].
 template <typename T>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, const int32_t* __restrict__ merges,
                                                            int64_t num_waves) {
   const int64_t v = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (v >= num_waves) return;
+  if (p.counts != nullptr && v >= (int64_t)max(sload(p.counts, 2), 0) * p.group) return;
   decode_merge_wave<T>(p, merges, v);
 }
 
@@ -114,6 +116,7 @@ int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, i
   p.num_items = (int)num_items;
   p.num_waves = (int)num_waves;
   p.wave_extra = wave_extra;
+  p.counts = nullptr;
   p.out = out;
   p.out_tok_stride = out_token_stride;
   p.out_head_stride = out_head_stride;
@@ -165,4 +168,37 @@ extern "C" int mva_paged_decode(const void* q, int64_t q_token_stride, int64_t q
   else return set_error("paged attention: dtype must be bf16 or fp16");
   if (rc) return rc;
   return launch_decode_merge(p, merges, num_merges, dtype, s);
+}
+
+extern "C" int mva_paged_decode_graph(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                                      const void* k_cache, const void* v_cache, int64_t num_pages,
+                                      int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
+                                      int64_t block_table_stride, const int32_t* seq_lens, const int32_t* counts,
+                                      const int32_t* items, int64_t item_capacity, const int32_t* wave_extra,
+                                      int64_t wave_capacity, int waves_per_group, const int32_t* merges,
+                                      int64_t merge_capacity, int64_t num_part_slots, void* out,
+                                      int64_t out_token_stride, int64_t out_head_stride, void* workspace,
+                                      int64_t workspace_bytes, int num_q_heads, int num_kv_heads, int head_dim,
+                                      int page_size, float softmax_scale, int dtype, void* stream) {
+  using namespace mva;
+  if (counts == nullptr || items == nullptr || wave_extra == nullptr)
+    return set_error("paged attention: graph launch needs counts, items and wave_extra");
+  if (wave_capacity <= 0 || wave_capacity > item_capacity)
+    return set_error("paged attention: graph launch needs 0 < wave_capacity <= item_capacity");
+  if (merge_capacity < 0 || (merge_capacity > 0 && merges == nullptr))
+    return set_error("paged attention: invalid merge capacity");
+  DecodeParams p;
+  int rc = fill_decode_params(p, q, q_token_stride, q_head_stride, k_cache, v_cache, num_pages, page_stride,
+                              token_stride, block_tables, block_table_stride, seq_lens, items, item_capacity,
+                              wave_capacity, wave_extra, merges, merge_capacity, num_part_slots, out,
+                              out_token_stride, out_head_stride, workspace, workspace_bytes, num_q_heads,
+                              num_kv_heads, head_dim, page_size, softmax_scale);
+  if (rc) return rc;
+  p.counts = counts;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == kBF16) rc = launch_paged_decode<__bf16>(p, waves_per_group, s);
+  else if (dtype == kF16) rc = launch_paged_decode<_Float16>(p, waves_per_group, s);
+  else return set_error("paged attention: dtype must be bf16 or fp16");
+  if (rc) return rc;
+  return launch_decode_merge(p, merges, merge_capacity, dtype, s);
 }

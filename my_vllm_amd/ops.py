@@ -187,6 +187,49 @@ def paged_decode(
     )
 
 
+def paged_decode_graph(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    counts: torch.Tensor,
+    items: torch.Tensor,
+    wave_extra: torch.Tensor,
+    waves_per_group: int,
+    merges: torch.Tensor,
+    num_part_slots: int,
+    out: torch.Tensor,
+    workspace: torch.Tensor,
+    softmax_scale: float,
+) -> None:
+    """Fixed-shape decode launch for HIP graph capture.
+
+    ``counts`` (int32 ``[3]`` on the device) holds this step's
+    ``{num_items, num_waves, num_merges}``; ``items`` ``[item_capacity, 8]``,
+    ``wave_extra`` ``[wave_capacity + 1]`` and ``merges`` ``[merge_capacity, 8]``
+    hold the piece-list plan.  Grids are sized by the capacities, so every
+    pointer and size stays fixed from one step to the next.
+    """
+    if min(counts.numel(), 3) != 3 or wave_extra.numel() < 2:
+        raise ValueError("graph decode needs 3 counts and at least one wavefront")
+    num_q_heads, head_dim = q.shape[1], q.shape[2]
+    num_pages, page_size, num_kv_heads = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
+    _native.call(
+        "mva_paged_decode_graph",
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k_cache.data_ptr(), v_cache.data_ptr(), num_pages, k_cache.stride(0), k_cache.stride(1),
+        block_tables.data_ptr(), block_tables.stride(0), seq_lens.data_ptr(),
+        counts.data_ptr(),
+        items.data_ptr(), items.shape[0], wave_extra.data_ptr(), wave_extra.numel() - 1, int(waves_per_group),
+        merges.data_ptr(), merges.shape[0], num_part_slots,
+        out.data_ptr(), out.stride(0), out.stride(1),
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+        num_q_heads, num_kv_heads, head_dim, page_size, float(softmax_scale),
+        _native.dtype_code(q.dtype), _native.stream_handle(q.device),
+    )
+
+
 def _paged_args(q, k_cache, v_cache, block_tables, seq_lens):
     return (
         q.data_ptr(), q.stride(0), q.stride(1),

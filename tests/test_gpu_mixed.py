@@ -1,7 +1,10 @@
 """MIXED batches: single-launch (MIXED_UNIFIED) and split (MIXED_SPLIT) routes.
 
-Both routes run the same device code paths, so their outputs must be
-bitwise identical; both are checked against the fp32 oracle (2e-2 / 1e-2).
+Both routes run the same prefill code, so the prefill rows must be bitwise
+identical; the split route's decode half runs the piece-list schedule (a
+different split-K partition than the single launch's claims), so decode
+rows agree within the attention tolerance.  Both are checked against the
+fp32 oracle (2e-2 / 1e-2).
 The split route writes ``out[:P]`` and ``out[P:]`` of one buffer without
 concatenation.
 """
@@ -29,8 +32,12 @@ def test_mixed_unified_and_split_match(gpu, monkeypatch, waves):
     out_s, plan_s = run_backend(batch, gpu, mode="split")
     assert plan_u.batch_type is BatchType.MIXED and plan_u.route is AttentionRoute.MIXED_UNIFIED
     assert plan_s.route is AttentionRoute.MIXED_SPLIT
-    assert torch.equal(out_u, out_s)
-    assert_attention_close(out_u, expected(batch))
+    prefill_rows = sum(q[:2])
+    assert torch.equal(out_u[:prefill_rows], out_s[:prefill_rows])
+    torch.testing.assert_close(out_u.float(), out_s.float(), atol=2e-2, rtol=1e-2)
+    ref = expected(batch)
+    assert_attention_close(out_u, ref)
+    assert_attention_close(out_s, ref)
 
 
 def test_all_single_token_mixed_batch(gpu):

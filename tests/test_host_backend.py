@@ -343,3 +343,60 @@ def test_decode_merge_list_names_every_split_segment_once(seed):
     assert np.all(merges[:, 3] == 0) and np.all(merges[:, 4] > 1)
     # Every merge's slots stay inside the plan's partial-slot count.
     assert np.all(merges[:, 5] + merges[:, 4] <= slots)
+
+
+# ---------------------------------------------------------------------------
+# Full-decode graph state (host side)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("seed", range(15))
+def test_graph_capacities_hold_every_fitting_piece_list_plan(seed):
+    from my_vllm_amd.attention_backend import graph_decode_capacities
+
+    rng = np.random.default_rng(900 + seed)
+    batch = int(rng.integers(1, 40))
+    width = int(rng.integers(1, 600))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    groups = int(rng.choice([1, 7, 256, 1024]))
+    caps = graph_decode_capacities(batch, batch * width, hkv, groups)
+    counts = rng.integers(1, width + 1, size=batch)
+    items, wave_extra, waves, slots = make_decode_plan_listed(counts, 0, 0, hkv, groups)
+    merges = ops.decode_merge_list(items)
+    assert items.shape[0] <= caps["item_capacity"]
+    assert waves <= caps["wave_capacity"] <= caps["item_capacity"]
+    assert merges.shape[0] <= caps["merge_capacity"]
+    assert slots <= caps["part_slot_capacity"]
+
+
+def test_graph_plan_buffer_layout_round_trips():
+    from my_vllm_amd.attention_backend import pack_graph_decode_plan, split_graph_plan_buffer
+
+    counts = np.array([3, 40, 1, 17])
+    items, wave_extra, waves, _ = make_decode_plan_listed(counts, 0, 0, 2, 5)
+    merges = ops.decode_merge_list(items)
+    buf = pack_graph_decode_plan(items, wave_extra, merges, 64, 12, 9)
+    c, it, we, mg = split_graph_plan_buffer(buf, 64, 12, 9)
+    assert c.tolist() == [items.shape[0], waves, merges.shape[0]]
+    assert np.array_equal(it[: items.shape[0]], items) and not it[items.shape[0]:].any()
+    assert np.array_equal(we[: waves + 1], wave_extra)
+    assert np.array_equal(mg[: merges.shape[0]], merges)
+    with pytest.raises(ValueError):
+        pack_graph_decode_plan(items, wave_extra, merges, items.shape[0] - 1, 12, 9)
+
+
+def test_graph_hooks_validate_like_the_reference():
+    backend = HostBackend(16, 8, 128, 16, torch.bfloat16)
+    assert backend.supports_full_decode_graph
+    with pytest.raises(ValueError):
+        backend.create_full_decode_graph_state(4, 64, "cpu")
+    with pytest.raises(TypeError):
+        backend.create_full_decode_graph_state(True, 64, "cpu")
+    with pytest.raises(ValueError):
+        backend.create_full_decode_graph_state(4, 3, "cpu")
+    plan = backend.build_plan(_common([1, 1], [20, 5], 0))
+    assert backend.full_decode_graph_metadata_fits(object(), plan) is False
+    with pytest.raises(ValueError, match="does not fit"):
+        backend.plan_full_decode_graph(object(), plan)
+    with pytest.raises(TypeError):
+        backend.activate_full_decode_graph(object())
+    backend.deactivate_full_decode_graph()
