@@ -243,6 +243,8 @@ def extra_measurements(device, steps: int):
     res["mixed_unified_roofline_frac"] = round(bound_ms / ms_u, 4)
     del batch
 
+    res.update(graph_vs_eager(device))
+
     # Long-context decode, Qwen3-32B (one layer's KV, ~10.7 GB).
     batch = config_long_decode(seed=4, device=device, rng_device="cuda")
     ms = attn_case(batch, 64, 8, iters=10)
@@ -252,6 +254,47 @@ def extra_measurements(device, steps: int):
     del batch
     torch.cuda.empty_cache()
     return res
+
+
+def graph_vs_eager(device, batch_size: int = 8, ctx: int = 512, steps: int = 200):
+    """Launch-bound decode step (KV store + attention) for a small batch at the
+    Qwen3-0.6B shape: eager launches vs one replay of a captured HIP graph of
+    the same two launches, per step (plan built once, as in steady decode)."""
+    from my_vllm_amd.attention import KVCacheStore
+    from my_vllm_amd.attention_backend import MI355XAttentionBackend
+    from my_vllm_amd.custom_op import CustomOpConfig
+    from my_vllm_amd.workloads import make_paged_batch
+
+    hq, hkv = 16, 8
+    batch = make_paged_batch(7, [1] * batch_size, [ctx] * batch_size, 0, hq, hkv)
+    common = to_device(batch, device)
+    q = batch.q.to(device)
+    k_new, v_new = batch.k_new.to(device), batch.v_new.to(device)
+    kc, vc = batch.k_cache.to(device), batch.v_cache.to(device)
+    backend = MI355XAttentionBackend(hq, hkv, 128, 16, torch.bfloat16)
+    store = KVCacheStore(CustomOpConfig(platform="cuda"))
+    plan = backend.build_plan(common)
+    empty = q.new_empty((0, hkv, 128))
+
+    def step(_):
+        store(k_new, v_new, kc, vc, common.slot_mapping)
+        backend.forward(q, empty, empty, kc, vc, plan)
+
+    eager_ms = time_launches(step, steps, 10)
+    state = backend.create_full_decode_graph_state(batch_size, sum(batch.block_counts), device)
+    backend.plan_full_decode_graph(state, plan)
+    backend.activate_full_decode_graph(state)
+    try:
+        step(0)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step(0)
+        torch.cuda.synchronize()
+    finally:
+        backend.deactivate_full_decode_graph()
+    graph_ms = time_launches(lambda i: graph.replay(), steps, 10)
+    return {"decode_step_8seq_eager_us": round(eager_ms * 1e3, 2), "decode_step_8seq_graph_us": round(graph_ms * 1e3, 2)}
 
 
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
