@@ -210,6 +210,20 @@ def extra_measurements(device, steps: int):
     res["silu_8192x51200_GBps"] = round(8192 * 51200 * 2 * 1.5 / ms / 1e6, 1)
     del x5
 
+    # RMSNorm and fused residual-add RMSNorm, 4096 tokens x 4096 (Qwen3-8B
+    # hidden), 8 rotating inputs (the residual pair: 512 MB > Infinity Cache).
+    from my_vllm_amd.workloads import silu_input as _randn_rows
+
+    xs = [_randn_rows(4096, 4096, seed=10 + i, device=device, rng_device="cuda") for i in range(8)]
+    rs = [_randn_rows(4096, 4096, seed=20 + i, device=device, rng_device="cuda") for i in range(8)]
+    w = torch.ones(4096, dtype=torch.bfloat16, device=device)
+    row_bytes = 4096 * 4096 * 2
+    ms = time_launches(lambda i: ops.rms_norm(xs[i % 8], w, 1e-6), 200, 20)
+    res["rms_norm_4096x4096_GBps"] = round(2 * row_bytes / ms / 1e6, 1)
+    ms = time_launches(lambda i: ops.fused_add_rms_norm(xs[i % 8], rs[i % 8], w, 1e-6), 200, 20)
+    res["fused_add_rms_norm_4096x4096_GBps"] = round(4 * row_bytes / ms / 1e6, 1)
+    del xs, rs
+
     def attn_case(batch, hq, hkv, mode="unified", iters=20):
         backend = MI355XAttentionBackend(hq, hkv, 128, 16, torch.bfloat16, attention_mode=mode)
         common = to_device(batch, device)

@@ -25,6 +25,7 @@ extern "C" {
 
 #define MVA_DTYPE_BF16 0
 #define MVA_DTYPE_F16 1
+#define MVA_DTYPE_F32 2 /* weights of mva_rms_norm / mva_fused_add_rms_norm only */
 
 /* Message of the calling thread's most recent failed call ("" if none). */
 const char* mva_last_error(void);
@@ -58,6 +59,35 @@ int mva_kv_store(const void* key, int64_t key_row_stride, const void* value,
                  int64_t value_row_stride, void* k_cache, void* v_cache, int64_t num_slots,
                  const void* slot_mapping, int slot_is_int64, int64_t num_tokens, int64_t row_elems,
                  int dtype, void* stream);
+
+/*
+ * RMSNorm over rows of `hidden` elements:
+ *   out[r] = T(T(x[r] * rsqrt(mean(x[r]^2) + eps)) * weight), fp32 statistics.
+ * x / out rows are x + r*x_row_stride / out + r*out_row_stride (elements,
+ * unit inner stride); out may equal x.  weight [hidden] has `weight_dtype`
+ * MVA_DTYPE_F32 or the input dtype.
+ * Replaces the reference's RMSNorm providers (nanovllm/layers/layernorm.py:
+ * 31-40 native path, :65-72 rms_norm provider; FlashInfer rmsnorm,
+ * nanovllm/layers/flashinfer_ops.py).
+ */
+int mva_rms_norm(const void* x, int64_t x_row_stride, const void* weight, void* out,
+                 int64_t out_row_stride, int64_t rows, int64_t hidden, float eps, int dtype,
+                 int weight_dtype, void* stream);
+
+/*
+ * Fused residual add + RMSNorm:
+ *   s = float(x) + float(residual); residual_out = T(s);
+ *   out = T(T(s * rsqrt(mean(s^2) + eps)) * weight)  (statistics of the fp32 sum).
+ * out may equal x and residual_out may equal residual (the in-place form of
+ * the reference's forward_inplace).
+ * Replaces the fused_add_rms_norm providers (nanovllm/layers/layernorm.py:
+ * 42-52 native path, :74-88 forward / forward_inplace).
+ */
+int mva_fused_add_rms_norm(const void* x, int64_t x_row_stride, const void* residual,
+                           int64_t residual_row_stride, const void* weight, void* out,
+                           int64_t out_row_stride, void* residual_out, int64_t residual_out_row_stride,
+                           int64_t rows, int64_t hidden, float eps, int dtype, int weight_dtype,
+                           void* stream);
 
 /*
  * Bytes of device workspace mva_paged_decode / mva_paged_mixed need for

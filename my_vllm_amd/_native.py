@@ -17,6 +17,8 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libmy_vllm_amd.so"
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1}
+# Weight element codes of the RMSNorm entry points (MVA_DTYPE_F32 = 2).
+WEIGHT_DTYPE_CODES = {**DTYPE_CODES, torch.float32: 2}
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -31,6 +33,12 @@ _SIGNATURES = {
     "mva_kv_store": (
         _i32,
         [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _i32, _i64, _i64, _i32, _c_void_p],
+    ),
+    "mva_rms_norm": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _i64, _f32, _i32, _i32, _c_void_p]),
+    "mva_fused_add_rms_norm": (
+        _i32,
+        [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _f32, _i32, _i32,
+         _c_void_p],
     ),
     "mva_decode_workspace_bytes": (_i64, [_i64, _i32, _i32]),
     "mva_paged_decode": (

@@ -12,7 +12,7 @@
 namespace mva {
 
 // Element codes shared with the host side (include/my_vllm_amd.h).
-enum DType : int { kBF16 = 0, kF16 = 1 };
+enum DType : int { kBF16 = 0, kF16 = 1, kF32 = 2 };
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));

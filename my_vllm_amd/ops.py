@@ -60,6 +60,79 @@ def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def _check_rows(name: str, x: torch.Tensor, hidden: int) -> None:
+    if not x.is_cuda:
+        raise RuntimeError(f"{name} expects a CUDA tensor")
+    if x.dtype not in _native.DTYPE_CODES:
+        raise RuntimeError(f"{name} only supports float16 and bfloat16")
+    if x.dim() < 1 or x.size(-1) != hidden or (x.numel() and x.stride(-1) != 1):
+        raise RuntimeError(f"{name} expects rows of {hidden} elements with unit stride")
+
+
+def _rows_view(x: torch.Tensor) -> tuple[int, int]:
+    """(rows, row stride) of ``x`` seen as ``[-1, hidden]`` without copying."""
+    if x.dim() == 1:
+        return 1, x.size(0)
+    flat = x.reshape(-1, x.size(-1))
+    if flat.data_ptr() != x.data_ptr() or (flat.size(0) > 1 and flat.stride(1) != 1):
+        raise RuntimeError("rms_norm expects rows addressable with one row stride")
+    return flat.size(0), flat.stride(0) if flat.size(0) > 1 else x.size(-1)
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    """RMSNorm of the last dimension (reference nanovllm/layers/layernorm.py:31-40)."""
+    hidden = weight.numel()
+    _check_rows("rms_norm", x, hidden)
+    if weight.dtype not in (x.dtype, torch.float32) or not weight.is_contiguous() or weight.device != x.device:
+        raise RuntimeError("rms_norm weight must be contiguous fp32 or the input dtype on the input device")
+    if out is None:
+        out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    if x.numel() == 0:
+        return out
+    rows, x_stride = _rows_view(x)
+    _, o_stride = _rows_view(out)
+    _native.call(
+        "mva_rms_norm", x.data_ptr(), x_stride, weight.data_ptr(), out.data_ptr(), o_stride, rows, hidden,
+        float(eps), _native.dtype_code(x.dtype), _native.WEIGHT_DTYPE_CODES[weight.dtype],
+        _native.stream_handle(x.device),
+    )
+    return out
+
+
+def fused_add_rms_norm(
+    x: torch.Tensor,
+    residual: torch.Tensor,
+    weight: torch.Tensor,
+    eps: float,
+    inplace: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(rms_norm(x + residual), x + residual)`` (reference layernorm.py:42-52);
+    ``inplace`` writes them into ``x`` and ``residual``."""
+    hidden = weight.numel()
+    _check_rows("fused_add_rms_norm", x, hidden)
+    if residual.shape != x.shape or residual.dtype != x.dtype or residual.device != x.device:
+        raise RuntimeError("fused_add_rms_norm expects residual with the shape and dtype of x")
+    if weight.dtype not in (x.dtype, torch.float32) or not weight.is_contiguous() or weight.device != x.device:
+        raise RuntimeError("rms_norm weight must be contiguous fp32 or the input dtype on the input device")
+    if inplace:
+        out, res_out = x, residual
+    else:
+        out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+        res_out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    if x.numel() == 0:
+        return out, res_out
+    rows, x_stride = _rows_view(x)
+    _, r_stride = _rows_view(residual)
+    _, o_stride = _rows_view(out)
+    _, ro_stride = _rows_view(res_out)
+    _native.call(
+        "mva_fused_add_rms_norm", x.data_ptr(), x_stride, residual.data_ptr(), r_stride, weight.data_ptr(),
+        out.data_ptr(), o_stride, res_out.data_ptr(), ro_stride, rows, hidden, float(eps),
+        _native.dtype_code(x.dtype), _native.WEIGHT_DTYPE_CODES[weight.dtype], _native.stream_handle(x.device),
+    )
+    return out, res_out
+
+
 def store_kvcache(
     key: torch.Tensor,
     value: torch.Tensor,

@@ -12,6 +12,10 @@ How each function is pinned (the tests under ``tests/test_oracle*.py``):
   (tests/test_custom_op_dispatch.py:75-95) plus brute force.
 * ``silu_and_mul_*``      — closed form g*sigmoid(g)*u evaluated with
   ``math.exp`` in Python, and torch's ``F.silu`` (a library routine).
+* ``rms_norm`` / ``fused_add_rms_norm`` — torch's ``F.rms_norm`` (a library
+  routine, single rounding: within 1 ulp), closed forms (constant rows give
+  sign(c) * w; a row of k copies of +-c), the fp32-sum statistics of the
+  fused form, and a planted statistics-of-the-rounded-sum mistake.
 * ``paged_attention`` / ``ragged_attention`` — pure-Python brute force on tiny
   inputs, ``F.scaled_dot_product_attention`` on the cacheless causal case,
   and invariants (one-key context returns V exactly; equal scores give the

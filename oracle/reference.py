@@ -39,6 +39,41 @@ def silu_and_mul_fused(x: torch.Tensor) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------------------
+# RMSNorm / fused residual-add RMSNorm
+# ---------------------------------------------------------------------------
+
+def rms_scaled(x32: torch.Tensor, eps: float, dtype: torch.dtype) -> torch.Tensor:
+    """The row scaled by its fp32 reciprocal RMS and rounded to ``dtype``
+    (the intermediate of nanovllm/layers/layernorm.py:35-38, before the
+    weight multiply)."""
+    r = torch.rsqrt(x32.pow(2).mean(dim=-1, keepdim=True) + eps)
+    return (x32 * r).to(dtype)
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """``T(T(x32 * rsqrt(mean(x32^2) + eps)) * w)`` with fp32 statistics.
+
+    Restates nanovllm/layers/layernorm.py:31-40: the scaled row is rounded to
+    the storage type, then multiplied by the weight (fp32 product, rounded
+    once more).
+    """
+    x32 = x.float()
+    r = torch.rsqrt(x32.pow(2).mean(dim=-1, keepdim=True) + eps)
+    return ((x32 * r).to(x.dtype).float() * weight.float()).to(x.dtype)
+
+
+def fused_add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float):
+    """``(rms_norm of the fp32 sum, T(sum))``.
+
+    Restates nanovllm/layers/layernorm.py:42-52: the statistics use the fp32
+    sum ``x + residual``, not the rounded residual that is returned.
+    """
+    s32 = x.float() + residual.float()
+    r = torch.rsqrt(s32.pow(2).mean(dim=-1, keepdim=True) + eps)
+    return ((s32 * r).to(x.dtype).float() * weight.float()).to(x.dtype), s32.to(x.dtype)
+
+
+# ---------------------------------------------------------------------------
 # slot_mapping KV store
 # ---------------------------------------------------------------------------
 

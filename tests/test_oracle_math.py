@@ -204,3 +204,62 @@ def test_split_k_lse_merge_equals_unsplit(cuts):
     merged = ref.lse_merge([o for o, _ in parts], [l for _, l in parts])
     torch.testing.assert_close(merged, full, atol=1e-5, rtol=1e-5)
     torch.testing.assert_close(torch.logsumexp(torch.stack([l for _, l in parts]), 0), full_lse)
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm oracle (nanovllm/layers/layernorm.py:31-52)
+# ---------------------------------------------------------------------------
+
+def _ulp(a, b):
+    from tests._util import max_ulp_diff
+
+    return max_ulp_diff(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rms_norm_oracle_matches_torch_library_rms_norm(dtype):
+    from oracle.reference import rms_norm
+
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(64, 1024, generator=g).to(dtype)
+    ones = torch.ones(1024, dtype=dtype)
+    lib = F.rms_norm(x.float(), (1024,), ones.float(), 1e-6).to(dtype)
+    assert _ulp(rms_norm(x, ones, 1e-6), lib) <= 1
+    w = (1 + 0.1 * torch.randn(1024, generator=g)).to(dtype)
+    lib = F.rms_norm(x.float(), (1024,), w.float(), 1e-6).to(dtype)
+    assert _ulp(rms_norm(x, w, 1e-6), lib) <= 2  # the oracle rounds twice, the library once
+
+
+def test_rms_norm_constant_rows_give_the_weight():
+    from oracle.reference import rms_norm
+
+    w = torch.randn(256, generator=torch.Generator().manual_seed(6)).bfloat16()
+    for c in (0.25, 1.0, -3.0, 100.0):
+        x = torch.full((3, 256), c).bfloat16()
+        expected = (w if c > 0 else -w).expand(3, -1)
+        assert torch.equal(rms_norm(x, w, 1e-6), expected)
+
+
+def test_fused_add_rms_norm_uses_fp32_sum_statistics():
+    from oracle.reference import fused_add_rms_norm, rms_norm
+
+    # x + residual = [257, 129] in fp32; bf16 rounds 257 to 256.  Normalising
+    # the fp32 sum (the reference) and normalising the rounded residual (a
+    # plausible mistake) differ in the second element.
+    x = torch.tensor([[256.0, 129.0]]).bfloat16()
+    residual = torch.tensor([[1.0, 0.0]]).bfloat16()
+    w = torch.ones(2).bfloat16()
+    out, res = fused_add_rms_norm(x, residual, w, 0.0)
+    assert res.tolist() == [[256.0, 129.0]]
+    s = [257.0, 129.0]
+    inv = 1.0 / ((s[0] ** 2 + s[1] ** 2) / 2) ** 0.5
+    assert out.tolist() == torch.tensor([[s[0] * inv, s[1] * inv]]).bfloat16().tolist()
+    planted = rms_norm(res, w, 0.0)
+    assert not torch.equal(out, planted)
+
+
+def test_rms_scaled_is_the_unit_weight_rms_norm():
+    from oracle.reference import rms_norm, rms_scaled
+
+    x = torch.randn(8, 96, generator=torch.Generator().manual_seed(7)).bfloat16()
+    assert torch.equal(rms_scaled(x.float(), 1e-6, torch.bfloat16), rms_norm(x, torch.ones(96).bfloat16(), 1e-6))
