@@ -90,6 +90,35 @@ int mva_fused_add_rms_norm(const void* x, int64_t x_row_stride, const void* resi
                            void* stream);
 
 /*
+ * Attention prologue in one launch, for num_tokens tokens:
+ *   1. when q_norm_weight / k_norm_weight are given (both or neither): per-head
+ *      RMSNorm of q and k over head_dim, T(T(x * rsqrt(mean(x^2) + eps)) * w);
+ *   2. neox rotary embedding of q and k with cos_sin_cache [max_position,
+ *      rotary_dim] fp32 (cos | sin) at positions [num_tokens] int64 (clamped to
+ *      [0, max_position)), fp32 products rounded once to `dtype`;
+ *   3. when k_cache is given: the slot_mapping store of the rotated k and of v
+ *      (caches contiguous [pages, page_size, num_kv_heads, head_dim],
+ *      num_slots = pages * page_size; slots outside [0, num_slots) skipped).
+ * q / k rows: base + token*token_stride + head*head_stride (elements, unit
+ * inner stride); outputs share the input strides and may alias the inputs.
+ * Requires head_dim == rotary_dim == 128.
+ * Replaces, as one launch, the reference's q_norm / k_norm RMSNorm, its
+ * RotaryEmbedding provider (nanovllm/layers/rotary_embedding.py:18-110,
+ * FlashInfer apply_rope_with_cos_sin_cache) and the KV store
+ * (nanovllm/layers/attention.py:44-101), called in sequence at
+ * nanovllm/models/qwen3.py:96-100 and attention.py:140-141.  With no norm
+ * weights and no cache it is the RotaryEmbedding provider alone.
+ */
+int mva_qk_norm_rope_store(const void* q_in, void* q_out, int64_t q_token_stride, int64_t q_head_stride,
+                           int num_q_heads, const void* k_in, void* k_out, int64_t k_token_stride,
+                           int64_t k_head_stride, const void* v, int64_t v_token_stride, int64_t v_head_stride,
+                           int num_kv_heads, const int64_t* positions, const float* cos_sin_cache,
+                           int64_t max_position, int rotary_dim, const void* q_norm_weight,
+                           const void* k_norm_weight, int weight_dtype, float eps, void* k_cache, void* v_cache,
+                           int64_t num_slots, const void* slot_mapping, int slot_is_int64, int64_t num_tokens,
+                           int head_dim, int dtype, void* stream);
+
+/*
  * Bytes of device workspace mva_paged_decode / mva_paged_mixed need for
  * `num_part_slots` split-K partial slots (a scheduler area of piece-claim
  * counters, then fp32 partial outputs and log-sum-exps), or -1 for invalid

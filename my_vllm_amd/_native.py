@@ -40,6 +40,18 @@ _SIGNATURES = {
         [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _f32, _i32, _i32,
          _c_void_p],
     ),
+    "mva_qk_norm_rope_store": (
+        _i32,
+        [
+            _c_void_p, _c_void_p, _i64, _i64, _i32,  # q_in, q_out, q strides, num_q_heads
+            _c_void_p, _c_void_p, _i64, _i64,  # k_in, k_out, k strides
+            _c_void_p, _i64, _i64, _i32,  # v, v strides, num_kv_heads
+            _c_void_p, _c_void_p, _i64, _i32,  # positions, cos_sin_cache, max_position, rotary_dim
+            _c_void_p, _c_void_p, _i32, _f32,  # q/k norm weights, weight dtype, eps
+            _c_void_p, _c_void_p, _i64, _c_void_p, _i32,  # k_cache, v_cache, num_slots, slot_mapping, int64 slots
+            _i64, _i32, _i32, _c_void_p,  # num_tokens, head_dim, dtype, stream
+        ],
+    ),
     "mva_decode_workspace_bytes": (_i64, [_i64, _i32, _i32]),
     "mva_paged_decode": (
         _i32,

@@ -133,6 +133,111 @@ def fused_add_rms_norm(
     return out, res_out
 
 
+def _check_heads(name: str, t: torch.Tensor, dtype: torch.dtype, device: torch.device) -> None:
+    if t.dim() != 3 or t.size(2) != HEAD_DIM or t.stride(2) != 1:
+        raise ValueError(f"{name} must be [tokens, heads, {HEAD_DIM}] with unit inner stride")
+    if t.dtype != dtype or t.device != device:
+        raise ValueError(f"{name} must share the query dtype and device")
+
+
+def qk_norm_rope_store(
+    positions: torch.Tensor,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    cos_sin_cache: torch.Tensor,
+    q_norm_weight: torch.Tensor | None = None,
+    k_norm_weight: torch.Tensor | None = None,
+    eps: float = 1e-6,
+    v: torch.Tensor | None = None,
+    k_cache: torch.Tensor | None = None,
+    v_cache: torch.Tensor | None = None,
+    slot_mapping: torch.Tensor | None = None,
+    q_out: torch.Tensor | None = None,
+    k_out: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-head q/k RMSNorm (when weights are given), neox RoPE and, when a
+    cache is given, the slot_mapping store of the rotated k and of v, in one
+    launch.  The reference runs these as separate ops
+    (nanovllm/models/qwen3.py:96-100, nanovllm/layers/attention.py:140-141).
+
+    ``q``/``k``/``v`` are ``[T, heads, 128]`` views (a packed qkv projection
+    works); outputs default to writing ``q`` and ``k`` in place.
+    ``cos_sin_cache`` is the RotaryEmbedding buffer, ``[max_pos, (1,) 128]``
+    fp32 (cos | sin); ``positions`` int64 ``[T]``.  Returns ``(q_out, k_out)``.
+    """
+    if not q.is_cuda:
+        raise RuntimeError("qk_norm_rope_store expects CUDA tensors")
+    dtype, device = q.dtype, q.device
+    _check_heads("query", q, dtype, device)
+    _check_heads("key", k, dtype, device)
+    num_tokens = q.size(0)
+    if k.size(0) != num_tokens or positions.shape != (num_tokens,) or positions.dtype != torch.int64:
+        raise ValueError("positions must be int64 [tokens] and key must have the query's token count")
+    if positions.device != device:
+        raise ValueError("positions must be on the query device")
+    table = cos_sin_cache.reshape(cos_sin_cache.size(0), -1)
+    if table.dtype != torch.float32 or table.size(1) != HEAD_DIM or not table.is_contiguous() or table.device != device:
+        raise ValueError(f"cos_sin_cache must be contiguous fp32 [max_position, {HEAD_DIM}] on the query device")
+    q_out = q if q_out is None else q_out
+    k_out = k if k_out is None else k_out
+    if q_out.shape != q.shape or q_out.stride() != q.stride() or k_out.shape != k.shape or k_out.stride() != k.stride():
+        raise ValueError("outputs must match the inputs' shape and strides")
+    weight_code = 0
+    if (q_norm_weight is None) != (k_norm_weight is None):
+        raise ValueError("give both q and k norm weights or neither")
+    if q_norm_weight is not None:
+        for w in (q_norm_weight, k_norm_weight):
+            if w.numel() != HEAD_DIM or not w.is_contiguous() or w.device != device or w.dtype not in (dtype, torch.float32):
+                raise ValueError(f"norm weights must be contiguous [{HEAD_DIM}] fp32 or the query dtype")
+        if q_norm_weight.dtype != k_norm_weight.dtype:
+            raise ValueError("q and k norm weights must share a dtype")
+        weight_code = _native.WEIGHT_DTYPE_CODES[q_norm_weight.dtype]
+    store = k_cache is not None
+    if store:
+        if v is None or v_cache is None or slot_mapping is None:
+            raise ValueError("the KV store needs v, v_cache and slot_mapping")
+        _check_heads("value", v, dtype, device)
+        num_kv = k.size(1)
+        for cache in (k_cache, v_cache):
+            if (cache.dtype != dtype or cache.device != device or cache.dim() != 4 or cache.size(2) != num_kv
+                    or cache.size(3) != HEAD_DIM or not cache.is_contiguous()):
+                raise ValueError("caches must be contiguous [pages, page, num_kv_heads, 128] in the query dtype")
+        if slot_mapping.dtype not in (torch.int32, torch.int64) or slot_mapping.numel() != num_tokens:
+            raise ValueError("slot_mapping must be int32/int64 with one slot per token")
+    if num_tokens == 0:
+        return q_out, k_out
+    _native.call(
+        "mva_qk_norm_rope_store",
+        q.data_ptr(), q_out.data_ptr(), q.stride(0), q.stride(1), q.size(1),
+        k.data_ptr(), k_out.data_ptr(), k.stride(0), k.stride(1),
+        v.data_ptr() if store else 0, v.stride(0) if store else 0, v.stride(1) if store else 0, k.size(1),
+        positions.data_ptr(), table.data_ptr(), table.size(0), HEAD_DIM,
+        q_norm_weight.data_ptr() if q_norm_weight is not None else 0,
+        k_norm_weight.data_ptr() if k_norm_weight is not None else 0, weight_code, float(eps),
+        k_cache.data_ptr() if store else 0, v_cache.data_ptr() if store else 0,
+        k_cache.size(0) * k_cache.size(1) if store else 0,
+        slot_mapping.data_ptr() if store else 0, int(store and slot_mapping.dtype == torch.int64),
+        num_tokens, HEAD_DIM, _native.dtype_code(dtype), _native.stream_handle(device),
+    )
+    return q_out, k_out
+
+
+def rotary_embedding(positions: torch.Tensor, query: torch.Tensor, key: torch.Tensor, cos_sin_cache: torch.Tensor,
+                     head_size: int = HEAD_DIM) -> tuple[torch.Tensor, torch.Tensor]:
+    """Neox RoPE into new tensors (nanovllm/layers/rotary_embedding.py:41-51);
+    ``query``/``key`` are ``[T, heads * head_size]`` or ``[T, heads, head_size]``."""
+    if head_size != HEAD_DIM:
+        raise ValueError(f"rotary embedding supports head_size {HEAD_DIM}")
+    q3 = query.view(query.size(0), -1, HEAD_DIM)
+    k3 = key.view(key.size(0), -1, HEAD_DIM)
+    q_out = torch.empty_like(q3)
+    k_out = torch.empty_like(k3)
+    if q_out.stride() != q3.stride() or k_out.stride() != k3.stride():
+        q3, k3 = q3.contiguous(), k3.contiguous()
+    qk_norm_rope_store(positions, q3, k3, cos_sin_cache, q_out=q_out, k_out=k_out)
+    return q_out.view(query.shape), k_out.view(key.shape)
+
+
 def store_kvcache(
     key: torch.Tensor,
     value: torch.Tensor,

@@ -16,6 +16,10 @@ How each function is pinned (the tests under ``tests/test_oracle*.py``):
   routine, single rounding: within 1 ulp), closed forms (constant rows give
   sign(c) * w; a row of k copies of +-c), the fp32-sum statistics of the
   fused form, and a planted statistics-of-the-rounded-sum mistake.
+* ``rope`` / ``qk_norm_rope`` — position 0 is the identity, the rotation of
+  each (x_j, x_{j+64}) pair matches a float64 complex multiplication by
+  e^{i p theta_j}, pair norms are preserved, and a planted interleaved
+  (GPT-J) pairing is caught.
 * ``paged_attention`` / ``ragged_attention`` — pure-Python brute force on tiny
   inputs, ``F.scaled_dot_product_attention`` on the cacheless causal case,
   and invariants (one-key context returns V exactly; equal scores give the

@@ -74,6 +74,35 @@ def fused_add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Te
 
 
 # ---------------------------------------------------------------------------
+# Rotary embedding and the fused attention prologue
+# ---------------------------------------------------------------------------
+
+def rope_cos_sin_cache(rotary_dim: int, max_position: int, base: float) -> torch.Tensor:
+    """``[max_position, 1, rotary_dim]`` fp32 cos | sin table
+    (nanovllm/layers/rotary_embedding.py:30-35)."""
+    inv_freq = 1.0 / (base ** (torch.arange(0, rotary_dim, 2, dtype=torch.float) / rotary_dim))
+    freqs = torch.einsum("i,j -> ij", torch.arange(max_position, dtype=torch.float), inv_freq)
+    return torch.cat((freqs.cos(), freqs.sin()), dim=-1).unsqueeze_(1)
+
+
+def rope(x: torch.Tensor, positions: torch.Tensor, cos_sin_cache: torch.Tensor) -> torch.Tensor:
+    """Neox rotation of ``x [T, H, D]``: halves x1, x2 -> (x1 c - x2 s, x2 c + x1 s),
+    fp32 products rounded once (rotary_embedding.py:7-15, 41-51)."""
+    cos, sin = cos_sin_cache[positions].chunk(2, dim=-1)  # [T, 1, D/2]
+    x1, x2 = torch.chunk(x.float(), 2, dim=-1)
+    return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
+
+
+def qk_norm_rope(q, k, positions, cos_sin_cache, q_norm_weight=None, k_norm_weight=None, eps=1e-6):
+    """q_norm / k_norm (per head) then RoPE, as Qwen3Attention.forward runs
+    them (nanovllm/models/qwen3.py:96-100)."""
+    if q_norm_weight is not None:
+        q = rms_norm(q, q_norm_weight, eps)
+        k = rms_norm(k, k_norm_weight, eps)
+    return rope(q, positions, cos_sin_cache), rope(k, positions, cos_sin_cache)
+
+
+# ---------------------------------------------------------------------------
 # slot_mapping KV store
 # ---------------------------------------------------------------------------
 

@@ -263,3 +263,37 @@ def test_rms_scaled_is_the_unit_weight_rms_norm():
 
     x = torch.randn(8, 96, generator=torch.Generator().manual_seed(7)).bfloat16()
     assert torch.equal(rms_scaled(x.float(), 1e-6, torch.bfloat16), rms_norm(x, torch.ones(96).bfloat16(), 1e-6))
+
+
+# ---------------------------------------------------------------------------
+# Rotary embedding oracle (nanovllm/layers/rotary_embedding.py)
+# ---------------------------------------------------------------------------
+
+def test_rope_position_zero_is_identity():
+    from oracle.reference import rope, rope_cos_sin_cache
+
+    x = torch.randn(3, 4, 128, generator=torch.Generator().manual_seed(8)).bfloat16()
+    table = rope_cos_sin_cache(128, 64, 1e6)
+    assert torch.equal(rope(x, torch.zeros(3, dtype=torch.long), table), x)
+
+
+def test_rope_is_complex_rotation_of_neox_pairs():
+    from oracle.reference import rope, rope_cos_sin_cache
+
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(5, 2, 128, generator=g).bfloat16()
+    pos = torch.tensor([0, 1, 17, 1000, 4095])
+    table = rope_cos_sin_cache(128, 4096, 1e6)
+    got = rope(x, pos, table).double()
+    theta = 1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float64) / 128))
+    z = torch.complex(x[..., :64].double(), x[..., 64:].double()) * torch.exp(1j * pos[:, None, None].double() * theta)
+    ref = torch.cat((z.real, z.imag), dim=-1)
+    assert (got - ref).abs().max().item() < 2 ** -6  # bf16 rounding of values up to ~4
+    # Each (j, j + 64) pair keeps its length.
+    pair = lambda t: t[..., :64] ** 2 + t[..., 64:] ** 2  # noqa: E731
+    torch.testing.assert_close(pair(got), pair(x.double()), atol=0.05, rtol=0.02)
+    # A planted interleaved (GPT-J) pairing is caught.
+    xi = x.float().reshape(5, 2, 64, 2)
+    cos, sin = table[pos].chunk(2, dim=-1)
+    planted = torch.stack((xi[..., 0] * cos - xi[..., 1] * sin, xi[..., 1] * cos + xi[..., 0] * sin), -1)
+    assert (planted.reshape(5, 2, 128).double() - ref).abs().max().item() > 0.1
