@@ -224,6 +224,8 @@ def extra_measurements(device, steps: int):
     res["fused_add_rms_norm_4096x4096_GBps"] = round(4 * row_bytes / ms / 1e6, 1)
     del xs, rs
 
+    res.update(prologue_fused_vs_separate(device))
+
     def attn_case(batch, hq, hkv, mode="unified", iters=20):
         backend = MI355XAttentionBackend(hq, hkv, 128, 16, torch.bfloat16, attention_mode=mode)
         common = to_device(batch, device)
@@ -268,6 +270,44 @@ def extra_measurements(device, steps: int):
     del batch
     torch.cuda.empty_cache()
     return res
+
+
+def prologue_fused_vs_separate(device, tokens: int = 4096, hq: int = 32, hkv: int = 8):
+    """Attention prologue at the Qwen3-8B shape for a 4096-token chunk: q/k
+    RMSNorm + RoPE + KV store as one launch vs the four separate ops."""
+    from my_vllm_amd import ops
+    from my_vllm_amd.custom_op import CustomOpConfig
+    from my_vllm_amd.rotary_embedding import RotaryEmbedding
+    from my_vllm_amd.workloads import silu_input as _randn_rows
+
+    width = (hq + 2 * hkv) * 128
+    qkv = _randn_rows(tokens, width, seed=30, device=device, rng_device="cuda")
+    q = qkv[:, : hq * 128].view(tokens, hq, 128)
+    k = qkv[:, hq * 128:(hq + hkv) * 128].view(tokens, hkv, 128)
+    v = qkv[:, (hq + hkv) * 128:].view(tokens, hkv, 128)
+    pos = torch.arange(tokens, device=device, dtype=torch.int64)
+    table = RotaryEmbedding(128, 128, 40960, 1e6, CustomOpConfig(platform="cuda")).cos_sin_cache.to(device)
+    w = torch.ones(128, dtype=torch.bfloat16, device=device)
+    pages = tokens // 16
+    kc = torch.zeros(pages, 16, hkv, 128, dtype=torch.bfloat16, device=device)
+    vc = torch.zeros_like(kc)
+    slots = torch.arange(tokens, dtype=torch.int32, device=device)
+
+    def fused(_):
+        ops.qk_norm_rope_store(pos, q, k, table, w, w, 1e-6, v, kc, vc, slots)
+
+    def separate(_):
+        qn = ops.rms_norm(q, w, 1e-6)
+        kn = ops.rms_norm(k, w, 1e-6)
+        qr, kr = ops.rotary_embedding(pos, qn, kn, table)
+        ops.store_kvcache(kr, v, kc, vc, slots)
+
+    fused_ms = time_launches(fused, 200, 20)
+    sep_ms = time_launches(separate, 200, 20)
+    moved = tokens * (hq + 2 * hkv) * 128 * 2 * 2  # read and write each q/k/v row once
+    return {"prologue_4096tok_fused_us": round(fused_ms * 1e3, 2),
+            "prologue_4096tok_separate_us": round(sep_ms * 1e3, 2),
+            "prologue_4096tok_fused_GBps": round(moved / fused_ms / 1e6, 1)}
 
 
 def graph_vs_eager(device, batch_size: int = 8, ctx: int = 512, steps: int = 200):

@@ -63,16 +63,18 @@ int mva_kv_store(const void* key, int64_t key_row_stride, const void* value,
 /*
  * RMSNorm over rows of `hidden` elements:
  *   out[r] = T(T(x[r] * rsqrt(mean(x[r]^2) + eps)) * weight), fp32 statistics.
- * x / out rows are x + r*x_row_stride / out + r*out_row_stride (elements,
- * unit inner stride); out may equal x.  weight [hidden] has `weight_dtype`
+ * Row r is row i = r % rows_per_group of group g = r / rows_per_group, at
+ * x + g*x_group_stride + i*x_row_stride (elements, unit inner stride; e.g.
+ * the heads of a [tokens, heads, head_dim] view of a packed projection), and
+ * likewise for out; out may equal x.  weight [hidden] has `weight_dtype`
  * MVA_DTYPE_F32 or the input dtype.
  * Replaces the reference's RMSNorm providers (nanovllm/layers/layernorm.py:
  * 31-40 native path, :65-72 rms_norm provider; FlashInfer rmsnorm,
  * nanovllm/layers/flashinfer_ops.py).
  */
-int mva_rms_norm(const void* x, int64_t x_row_stride, const void* weight, void* out,
-                 int64_t out_row_stride, int64_t rows, int64_t hidden, float eps, int dtype,
-                 int weight_dtype, void* stream);
+int mva_rms_norm(const void* x, int64_t x_group_stride, int64_t x_row_stride, const void* weight, void* out,
+                 int64_t out_group_stride, int64_t out_row_stride, int64_t rows, int64_t rows_per_group,
+                 int64_t hidden, float eps, int dtype, int weight_dtype, void* stream);
 
 /*
  * Fused residual add + RMSNorm:

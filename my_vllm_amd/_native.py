@@ -34,7 +34,10 @@ _SIGNATURES = {
         _i32,
         [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _i32, _i64, _i64, _i32, _c_void_p],
     ),
-    "mva_rms_norm": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _i64, _f32, _i32, _i32, _c_void_p]),
+    "mva_rms_norm": (
+        _i32,
+        [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _c_void_p],
+    ),
     "mva_fused_add_rms_norm": (
         _i32,
         [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _f32, _i32, _i32,

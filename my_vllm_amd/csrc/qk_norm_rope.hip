@@ -14,11 +14,13 @@
 // Queries and keys are written to their output rows (which may alias the
 // inputs); V is only copied into the cache.
 //
-// One wavefront per (token, head) row of q, k or v; lane j owns elements j
-// and j + 64 of the 128-wide head, exactly the pair the rotation mixes, so
-// the norm's sum of squares is the only cross-lane step.
+// Sixteen lanes per (token, head) row of q, k or v; each lane owns four
+// elements of each half of the 128-wide head, so the pairs the rotation mixes
+// sit in one lane and the norm's sum of squares is the only cross-lane step.
 #include "mva_capi.h"
 #include "mva_common.h"
+
+#include <algorithm>
 
 namespace mva {
 namespace {
@@ -49,75 +51,124 @@ struct PrologueArgs {
   int64_t num_tokens;
 };
 
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct Vec4;
+template <>
+struct Vec4<__bf16> {
+  typedef __bf16 type __attribute__((ext_vector_type(4)));
+};
+template <>
+struct Vec4<_Float16> {
+  typedef _Float16 type __attribute__((ext_vector_type(4)));
+};
+
 template <typename W>
-__device__ inline float wget(const void* w, int i) {
-  return (float)((const W*)w)[i];
+__device__ inline f32x4v load_w4(const void* w, int i) {
+  if constexpr (sizeof(W) == 4) {
+    return *reinterpret_cast<const f32x4v*>((const float*)w + i);
+  } else {
+    const typename Vec4<W>::type v = *reinterpret_cast<const typename Vec4<W>::type*>((const W*)w + i);
+    return f32x4v{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+  }
 }
 
+// Four (token, head) rows per wavefront: the 16 lanes of group g = lane / 16
+// own row 4q + g of the current quad q; lane c = lane % 16 holds elements
+// 4c .. 4c+3 of the first half of the head and 64 + 4c .. 64 + 4c + 3 of the
+// second (the pairs the rotation mixes), loaded and stored 8 bytes at a time.
+// Rows r of a token: [0, Hq) queries, [Hq, Hq + Hkv) keys, then (with a
+// store) [Hq + Hkv, Hq + 2 Hkv) values.  A grid-stride loop over quads.
 template <typename T, typename W>
 __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(PrologueArgs a) {
   // Separate fp32 multiplies and adds, as torch evaluates the rotation (no
   // fused multiply-add contraction).
 #pragma clang fp contract(off)
+  typedef typename Vec4<T>::type V4;
   const int lane = threadIdx.x & 63;
+  const int g = lane >> 4;
+  const int c4 = 4 * (lane & 15);
   const int rows_per_tok = a.num_q_heads + a.num_kv_heads + (a.k_cache != nullptr ? a.num_kv_heads : 0);
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= a.num_tokens * rows_per_tok) return;
-  const int64_t t = row / rows_per_tok;
-  const int r = (int)(row - t * rows_per_tok);
-  int64_t slot = -1;
-  if (a.k_cache != nullptr) {
-    slot = a.slot_is_int64 ? ((const int64_t*)a.slots)[t] : (int64_t)((const int32_t*)a.slots)[t];
-    if (slot >= a.num_slots) slot = -1;
-  }
-  const int64_t cache_row = (slot >= 0) ? slot * a.num_kv_heads : 0;  // rows of [slots * Hkv, 128]
-
-  if (r >= a.num_q_heads + a.num_kv_heads) {  // V: copy into the cache
-    if (slot < 0) return;
-    const int h = r - a.num_q_heads - a.num_kv_heads;
-    const T* src = (const T*)a.v + t * a.v_tok_stride + h * a.v_head_stride;
-    T* dst = (T*)a.v_cache + (cache_row + h) * kRopeDim;
-    dst[lane] = src[lane];
-    dst[lane + 64] = src[lane + 64];
-    return;
-  }
-  const bool is_q = r < a.num_q_heads;
-  const int h = is_q ? r : r - a.num_q_heads;
-  const T* src = is_q ? (const T*)a.q_in + t * a.q_tok_stride + h * a.q_head_stride
-                      : (const T*)a.k_in + t * a.k_tok_stride + h * a.k_head_stride;
-  float x1 = (float)src[lane];
-  float x2 = (float)src[lane + 64];
-  const void* w = is_q ? a.q_norm_w : a.k_norm_w;
-  if (w != nullptr) {
-    float ss = x1 * x1 + x2 * x2;
+  const int64_t total = a.num_tokens * rows_per_tok;
+  const int64_t waves = (int64_t)gridDim.x * 4;
+  for (int64_t quad = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); quad * 4 < total; quad += waves) {
+    const int64_t row = quad * 4 + g;
+    if (row >= total) continue;  // a whole 16-lane group: no shuffle partner is lost
+    const int64_t t = row / rows_per_tok;
+    const int r = (int)(row - t * rows_per_tok);
+    int64_t slot = -1;
+    if (a.k_cache != nullptr) {
+      slot = a.slot_is_int64 ? ((const int64_t*)a.slots)[t] : (int64_t)((const int32_t*)a.slots)[t];
+      if (slot >= a.num_slots) slot = -1;
+    }
+    const int64_t cache_row = (slot >= 0) ? slot * a.num_kv_heads : 0;  // rows of [slots * Hkv, 128]
+    if (r >= a.num_q_heads + a.num_kv_heads) {  // V: copy into the cache
+      if (slot >= 0) {
+        const int h = r - a.num_q_heads - a.num_kv_heads;
+        const T* src = (const T*)a.v + t * a.v_tok_stride + h * a.v_head_stride;
+        T* dst = (T*)a.v_cache + (cache_row + h) * kRopeDim;
+        *reinterpret_cast<V4*>(dst + c4) = *reinterpret_cast<const V4*>(src + c4);
+        *reinterpret_cast<V4*>(dst + 64 + c4) = *reinterpret_cast<const V4*>(src + 64 + c4);
+      }
+      continue;
+    }
+    const bool is_q = r < a.num_q_heads;
+    const int h = is_q ? r : r - a.num_q_heads;
+    const T* src = is_q ? (const T*)a.q_in + t * a.q_tok_stride + h * a.q_head_stride
+                        : (const T*)a.k_in + t * a.k_tok_stride + h * a.k_head_stride;
+    const V4 lo = *reinterpret_cast<const V4*>(src + c4);
+    const V4 hi = *reinterpret_cast<const V4*>(src + 64 + c4);
+    float x1[4], x2[4];
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-    const float rr = 1.0f / __builtin_sqrtf(ss / (float)kRopeDim + a.eps);
-    x1 = (float)(T)((float)(T)(x1 * rr) * wget<W>(w, lane));
-    x2 = (float)(T)((float)(T)(x2 * rr) * wget<W>(w, lane + 64));
-  }
-  int64_t pos = a.positions[t];
-  pos = pos < 0 ? 0 : (pos >= a.max_position ? a.max_position - 1 : pos);  // stay in bounds
-  const float c = a.cos_sin[pos * kRopeDim + lane];
-  const float s = a.cos_sin[pos * kRopeDim + 64 + lane];
-  const T y1 = (T)(x1 * c - x2 * s);
-  const T y2 = (T)(x2 * c + x1 * s);
-  T* dst = is_q ? (T*)a.q_out + t * a.q_tok_stride + h * a.q_head_stride
-                : (T*)a.k_out + t * a.k_tok_stride + h * a.k_head_stride;
-  dst[lane] = y1;
-  dst[lane + 64] = y2;
-  if (!is_q && slot >= 0) {
-    T* kd = (T*)a.k_cache + (cache_row + h) * kRopeDim;
-    kd[lane] = y1;
-    kd[lane + 64] = y2;
+    for (int e = 0; e < 4; ++e) {
+      x1[e] = (float)lo[e];
+      x2[e] = (float)hi[e];
+    }
+    const void* w = is_q ? a.q_norm_w : a.k_norm_w;
+    if (w != nullptr) {
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ss += x1[e] * x1[e] + x2[e] * x2[e];
+#pragma unroll
+      for (int off = 8; off > 0; off >>= 1) ss += __shfl_xor(ss, off);  // within the 16-lane group
+      const float rr = 1.0f / __builtin_sqrtf(ss / (float)kRopeDim + a.eps);
+      const f32x4v w1 = load_w4<W>(w, c4);
+      const f32x4v w2 = load_w4<W>(w, 64 + c4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x1[e] = (float)(T)((float)(T)(x1[e] * rr) * w1[e]);
+        x2[e] = (float)(T)((float)(T)(x2[e] * rr) * w2[e]);
+      }
+    }
+    int64_t pos = a.positions[t];
+    pos = pos < 0 ? 0 : (pos >= a.max_position ? a.max_position - 1 : pos);  // stay in bounds
+    const f32x4v cs = *reinterpret_cast<const f32x4v*>(a.cos_sin + pos * kRopeDim + c4);
+    const f32x4v sn = *reinterpret_cast<const f32x4v*>(a.cos_sin + pos * kRopeDim + 64 + c4);
+    V4 y1, y2;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      y1[e] = (T)(x1[e] * cs[e] - x2[e] * sn[e]);
+      y2[e] = (T)(x2[e] * cs[e] + x1[e] * sn[e]);
+    }
+    T* dst = is_q ? (T*)a.q_out + t * a.q_tok_stride + h * a.q_head_stride
+                  : (T*)a.k_out + t * a.k_tok_stride + h * a.k_head_stride;
+    *reinterpret_cast<V4*>(dst + c4) = y1;
+    *reinterpret_cast<V4*>(dst + 64 + c4) = y2;
+    if (!is_q && slot >= 0) {
+      T* kd = (T*)a.k_cache + (cache_row + h) * kRopeDim;
+      *reinterpret_cast<V4*>(kd + c4) = y1;
+      *reinterpret_cast<V4*>(kd + 64 + c4) = y2;
+    }
   }
 }
 
 template <typename T>
 int launch_prologue(const PrologueArgs& a, int weight_dtype, hipStream_t s) {
   const int64_t rows = a.num_tokens * (a.num_q_heads + a.num_kv_heads + (a.k_cache != nullptr ? a.num_kv_heads : 0));
-  const int64_t blocks = (rows + 3) / 4;
-  if (blocks > 0x7fffffffLL) return set_error("qk_norm_rope: too many rows");
+  const int64_t quads = (rows + 3) / 4;
+  // Four quads per workgroup pass; at most 8 resident workgroups per CU's worth.
+  const int64_t blocks = std::min<int64_t>((quads + 3) / 4, 256 * 16);
   if (weight_dtype == kF32)
     hipLaunchKernelGGL((qk_norm_rope_store_kernel<T, float>), dim3((uint32_t)blocks), dim3(256), 0, s, a);
   else
@@ -150,6 +201,16 @@ extern "C" int mva_qk_norm_rope_store(const void* q_in, void* q_out, int64_t q_t
     return set_error("qk_norm_rope: the store needs v, v_cache and slot_mapping");
   if (q_norm_weight != nullptr && weight_dtype != kF32 && weight_dtype != dtype)
     return set_error("qk_norm_rope: norm weights must be fp32 or the input dtype");
+  const uint64_t align = (uint64_t)(uintptr_t)q_in | (uint64_t)(uintptr_t)q_out | (uint64_t)(uintptr_t)k_in |
+                         (uint64_t)(uintptr_t)k_out | (uint64_t)(uintptr_t)v | (uint64_t)(uintptr_t)k_cache |
+                         (uint64_t)(uintptr_t)v_cache | (uint64_t)(q_token_stride | q_head_stride | k_token_stride |
+                                                                k_head_stride | v_token_stride | v_head_stride) * 2 |
+                         (uint64_t)(uintptr_t)cos_sin_cache | (uint64_t)(uintptr_t)q_norm_weight |
+                         (uint64_t)(uintptr_t)k_norm_weight;
+  if (align % 8 != 0)
+    return set_error("qk_norm_rope: buffers and strides must be 8-byte aligned");
+  if (((uint64_t)(uintptr_t)cos_sin_cache | (uint64_t)(uintptr_t)q_norm_weight | (uint64_t)(uintptr_t)k_norm_weight) % 16)
+    return set_error("qk_norm_rope: cos_sin_cache and norm weights must be 16-byte aligned");
   PrologueArgs a{q_in, q_out, q_token_stride, q_head_stride, k_in, k_out, k_token_stride, k_head_stride,
                  v, v_token_stride, v_head_stride, num_q_heads, num_kv_heads, positions, cos_sin_cache,
                  max_position, q_norm_weight, k_norm_weight, eps, k_cache, v_cache, num_slots, slot_mapping,

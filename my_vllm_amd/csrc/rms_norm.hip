@@ -21,9 +21,12 @@
 namespace mva {
 namespace {
 
+// Row r of a call is row (r % rows_per_group) of group (r / rows_per_group):
+// x + (r / rows_per_group) * x_group_stride + (r % rows_per_group) * x_stride
+// (likewise for out; the fused form uses one group per row).
 struct RmsArgs {
   const void* x;
-  int64_t x_stride;  // elements between rows
+  int64_t x_stride;  // elements between rows of a group
   const void* residual;  // nullptr: plain RMSNorm
   int64_t res_stride;
   const void* weight;
@@ -34,7 +37,15 @@ struct RmsArgs {
   int64_t rows;
   int hidden;
   float eps;
+  int64_t rows_per_group;
+  int64_t x_group_stride;
+  int64_t out_group_stride;
 };
+
+__device__ inline int64_t row_offset(int64_t r, int64_t per_group, int64_t group_stride, int64_t stride) {
+  const int64_t g = r / per_group;
+  return g * group_stride + (r - g * per_group) * stride;
+}
 
 __device__ inline float wave_sum(float v) {
 #pragma unroll
@@ -76,7 +87,7 @@ __global__ __launch_bounds__(256) void rms_norm_vec_kernel(RmsArgs a) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= a.rows) return;
   const int nvec = a.hidden >> 3;
-  const T* xr = (const T*)a.x + row * a.x_stride;
+  const T* xr = (const T*)a.x + row_offset(row, a.rows_per_group, a.x_group_stride, a.x_stride);
   const T* rr = kAdd ? (const T*)a.residual + row * a.res_stride : nullptr;
   float v[kChunks][8];
   float ss = 0.f;
@@ -98,7 +109,7 @@ __global__ __launch_bounds__(256) void rms_norm_vec_kernel(RmsArgs a) {
   }
   ss = wave_sum(ss);
   const float r = 1.0f / __builtin_sqrtf(ss / (float)a.hidden + a.eps);
-  T* orow = (T*)a.out + row * a.out_stride;
+  T* orow = (T*)a.out + row_offset(row, a.rows_per_group, a.out_group_stride, a.out_stride);
   T* ro = kAdd ? (T*)a.residual_out + row * a.res_out_stride : nullptr;
   const W* w = (const W*)a.weight;
 #pragma unroll
@@ -128,7 +139,7 @@ __global__ __launch_bounds__(256) void rms_norm_scalar_kernel(RmsArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= a.rows) return;
-  const T* xr = (const T*)a.x + row * a.x_stride;
+  const T* xr = (const T*)a.x + row_offset(row, a.rows_per_group, a.x_group_stride, a.x_stride);
   const T* rr = kAdd ? (const T*)a.residual + row * a.res_stride : nullptr;
   float ss = 0.f;
   for (int i = lane; i < a.hidden; i += 64) {
@@ -138,7 +149,7 @@ __global__ __launch_bounds__(256) void rms_norm_scalar_kernel(RmsArgs a) {
   }
   ss = wave_sum(ss);
   const float r = 1.0f / __builtin_sqrtf(ss / (float)a.hidden + a.eps);
-  T* orow = (T*)a.out + row * a.out_stride;
+  T* orow = (T*)a.out + row_offset(row, a.rows_per_group, a.out_group_stride, a.out_stride);
   T* ro = kAdd ? (T*)a.residual_out + row * a.res_out_stride : nullptr;
   const W* w = (const W*)a.weight;
   for (int i = lane; i < a.hidden; i += 64) {
@@ -156,7 +167,9 @@ int launch_rms(const RmsArgs& a, hipStream_t s) {
   if (blocks > 0x7fffffffLL) return set_error("rms_norm: too many rows");
   const dim3 grid((uint32_t)blocks), block(256);
   uint64_t bits = (uint64_t)(uintptr_t)a.x | (uint64_t)(uintptr_t)a.out | (uint64_t)(uintptr_t)a.weight |
-                  (uint64_t)(a.x_stride * (int64_t)sizeof(T)) | (uint64_t)(a.out_stride * (int64_t)sizeof(T));
+                  (uint64_t)(a.x_stride * (int64_t)sizeof(T)) | (uint64_t)(a.out_stride * (int64_t)sizeof(T)) |
+                  (uint64_t)(a.x_group_stride * (int64_t)sizeof(T)) |
+                  (uint64_t)(a.out_group_stride * (int64_t)sizeof(T));
   if (kAdd)
     bits |= (uint64_t)(uintptr_t)a.residual | (uint64_t)(uintptr_t)a.residual_out |
             (uint64_t)(a.res_stride * (int64_t)sizeof(T)) | (uint64_t)(a.res_out_stride * (int64_t)sizeof(T));
@@ -189,12 +202,15 @@ int dispatch(const RmsArgs& a, int dtype, int weight_dtype, hipStream_t s) {
 }  // namespace
 }  // namespace mva
 
-extern "C" int mva_rms_norm(const void* x, int64_t x_row_stride, const void* weight, void* out,
-                            int64_t out_row_stride, int64_t rows, int64_t hidden, float eps, int dtype,
-                            int weight_dtype, void* stream) {
+extern "C" int mva_rms_norm(const void* x, int64_t x_group_stride, int64_t x_row_stride, const void* weight,
+                            void* out, int64_t out_group_stride, int64_t out_row_stride, int64_t rows,
+                            int64_t rows_per_group, int64_t hidden, float eps, int dtype, int weight_dtype,
+                            void* stream) {
   using namespace mva;
   if (hidden > 0x7fffffffLL) return set_error("rms_norm: hidden too large");
-  RmsArgs a{x, x_row_stride, nullptr, 0, weight, out, out_row_stride, nullptr, 0, rows, (int)hidden, eps};
+  if (rows_per_group <= 0) return set_error("rms_norm: rows_per_group must be positive");
+  RmsArgs a{x, x_row_stride, nullptr, 0, weight, out, out_row_stride, nullptr, 0, rows, (int)hidden, eps,
+            rows_per_group, x_group_stride, out_group_stride};
   return dispatch<false>(a, dtype, weight_dtype, (hipStream_t)stream);
 }
 
@@ -207,6 +223,6 @@ extern "C" int mva_fused_add_rms_norm(const void* x, int64_t x_row_stride, const
   if (hidden > 0x7fffffffLL) return set_error("rms_norm: hidden too large");
   if (residual == nullptr || residual_out == nullptr) return set_error("rms_norm: missing residual buffers");
   RmsArgs a{x, x_row_stride, residual, residual_row_stride, weight, out, out_row_stride,
-            residual_out, residual_out_row_stride, rows, (int)hidden, eps};
+            residual_out, residual_out_row_stride, rows, (int)hidden, eps, 1, x_row_stride, out_row_stride};
   return dispatch<true>(a, dtype, weight_dtype, (hipStream_t)stream);
 }

@@ -79,22 +79,45 @@ def _rows_view(x: torch.Tensor) -> tuple[int, int]:
     return flat.size(0), flat.stride(0) if flat.size(0) > 1 else x.size(-1)
 
 
+def _grouped_rows(x: torch.Tensor) -> tuple[int, int, int, int]:
+    """(groups, rows per group, group stride, row stride) of ``x`` as
+    ``[G, R, hidden]`` without copying: a 2-D (or mergeable) tensor is one row
+    per group; ``[tokens, heads, hidden]`` views of a packed projection keep
+    their token and head strides."""
+    if x.dim() <= 2:
+        rows, stride = _rows_view(x)
+        return rows, 1, stride, stride
+    lead = x.reshape(-1, x.size(-2), x.size(-1)) if x.dim() > 3 else x
+    if lead.data_ptr() != x.data_ptr() or (lead.numel() and lead.stride(2) != 1):
+        raise RuntimeError("rms_norm expects [..., rows, hidden] with unit inner stride")
+    return lead.size(0), lead.size(1), lead.stride(0), lead.stride(1)
+
+
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor | None = None) -> torch.Tensor:
-    """RMSNorm of the last dimension (reference nanovllm/layers/layernorm.py:31-40)."""
+    """RMSNorm of the last dimension (reference nanovllm/layers/layernorm.py:31-40).
+
+    ``x`` may be a strided view such as the ``[tokens, heads, head_dim]`` query
+    slice of a packed qkv projection (the reference's q_norm input); the
+    result is a new contiguous tensor unless ``out`` is given.
+    """
     hidden = weight.numel()
     _check_rows("rms_norm", x, hidden)
     if weight.dtype not in (x.dtype, torch.float32) or not weight.is_contiguous() or weight.device != x.device:
         raise RuntimeError("rms_norm weight must be contiguous fp32 or the input dtype on the input device")
     if out is None:
         out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    if out.shape != x.shape:
+        raise RuntimeError("rms_norm output must have the input shape")
     if x.numel() == 0:
         return out
-    rows, x_stride = _rows_view(x)
-    _, o_stride = _rows_view(out)
+    groups, per_group, x_gs, x_rs = _grouped_rows(x)
+    o_groups, o_per_group, o_gs, o_rs = _grouped_rows(out)
+    if (o_groups, o_per_group) != (groups, per_group):
+        raise RuntimeError("rms_norm output rows must match the input rows")
     _native.call(
-        "mva_rms_norm", x.data_ptr(), x_stride, weight.data_ptr(), out.data_ptr(), o_stride, rows, hidden,
-        float(eps), _native.dtype_code(x.dtype), _native.WEIGHT_DTYPE_CODES[weight.dtype],
-        _native.stream_handle(x.device),
+        "mva_rms_norm", x.data_ptr(), x_gs, x_rs, weight.data_ptr(), out.data_ptr(), o_gs, o_rs,
+        groups * per_group, per_group, hidden, float(eps), _native.dtype_code(x.dtype),
+        _native.WEIGHT_DTYPE_CODES[weight.dtype], _native.stream_handle(x.device),
     )
     return out
 

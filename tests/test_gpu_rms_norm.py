@@ -111,3 +111,21 @@ def test_custom_op_providers(gpu):
     assert alias.rms_provider_name == "hip"
     with pytest.raises(RuntimeError, match="CUDA tensor"):
         ops.rms_norm(x, w.to(gpu), 1e-6)
+
+
+def test_rms_norm_of_head_views_of_a_packed_projection(gpu):
+    # The reference applies q_norm / k_norm to [tokens, heads, head_dim] views
+    # of the packed qkv projection (token stride != heads * head_dim).
+    tokens, hq, hkv = 19, 32, 8
+    qkv = torch.randn(tokens, (hq + 2 * hkv) * 128, generator=torch.Generator().manual_seed(18)).bfloat16()
+    w = (1 + 0.2 * torch.randn(128, generator=torch.Generator().manual_seed(19))).bfloat16()
+    q = qkv[:, : hq * 128].view(tokens, hq, 128)
+    k = qkv[:, hq * 128:(hq + hkv) * 128].view(tokens, hkv, 128)
+    qd = qkv.to(gpu)[:, : hq * 128].view(tokens, hq, 128)
+    kd = qkv.to(gpu)[:, hq * 128:(hq + hkv) * 128].view(tokens, hkv, 128)
+    assert_rms_matches(ops.rms_norm(qd, w.to(gpu), 1e-6), q.float(), w, 1e-6)
+    assert_rms_matches(ops.rms_norm(kd, w.to(gpu), 1e-6), k.float(), w, 1e-6)
+    norm = RMSNorm(128, 1e-6, CustomOpConfig(platform="cuda", dtype=torch.bfloat16)).to(gpu, torch.bfloat16)
+    with torch.no_grad():
+        norm.weight.copy_(w)
+    assert_rms_matches(norm(qd), q.float(), w, 1e-6)
