@@ -221,39 +221,6 @@ def _has_cache(cache: torch.Tensor | None) -> bool:
     return isinstance(cache, torch.Tensor) and cache.numel() > 0
 
 
-def _torch_sdpa_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, common: Any) -> torch.Tensor:
-    """Cacheless causal varlen attention, one SDPA call per sequence.
-
-    Restates the reference's dependency-free warmup path
-    (nanovllm/layers/attention_backend.py:1580-1624).  Operands are made
-    contiguous before SDPA so no batched product sees a transposed bf16 view.
-    """
-    if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
-        raise ValueError("cacheless attention expects rank-3 Q/K/V")
-    if k.shape != v.shape:
-        raise ValueError("cacheless key and value shapes must match")
-    if q.size(0) != k.size(0):
-        raise ValueError("cacheless warmup requires matching query and KV token counts")
-    if q.size(1) % k.size(1):
-        raise ValueError("query head count must be divisible by KV head count")
-    starts = common.query_start_loc
-    boundaries = starts.cpu().tolist()
-    kv_repeat = q.size(1) // k.size(1)
-    outputs = []
-    for start, end in zip(boundaries[:-1], boundaries[1:]):
-        q_seq = q[start:end].transpose(0, 1).unsqueeze(0).contiguous()
-        k_seq = k[start:end].transpose(0, 1).unsqueeze(0)
-        v_seq = v[start:end].transpose(0, 1).unsqueeze(0)
-        if kv_repeat != 1:
-            k_seq = k_seq.repeat_interleave(kv_repeat, dim=1)
-            v_seq = v_seq.repeat_interleave(kv_repeat, dim=1)
-        output = F.scaled_dot_product_attention(
-            q_seq, k_seq.contiguous(), v_seq.contiguous(), is_causal=True, scale=1.0 / sqrt(q.size(-1))
-        )
-        outputs.append(output.squeeze(0).transpose(0, 1))
-    return torch.cat(outputs, dim=0) if outputs else torch.empty_like(q)
-
-
 # --------------------------------------------------------------------------
 # MI355X backend.
 # --------------------------------------------------------------------------
@@ -940,10 +907,10 @@ class MI355XAttentionBackendMixin:
                 raise ValueError("MI355X warmup route requires an empty KV cache")
             if not metadata.is_cacheless:
                 raise ValueError("MI355X warmup route requires cacheless metadata")
-            output = _torch_sdpa_varlen(q, k, v, plan.common)
-            scratch = self._get_reusable_attention_output(q)
-            scratch.copy_(output)
-            return scratch
+            self._check_cacheless_inputs(q, k, v)
+            output = self._get_reusable_attention_output(q)
+            self._run_warmup(q, k, v, plan.common, output)
+            return output
 
         expected = {
             Route.PREFILL: Batch.PURE_PREFILL,
@@ -1115,6 +1082,61 @@ class MI355XAttentionBackendMixin:
 
     def deactivate_full_decode_graph(self) -> None:
         self._active_graph_state = None
+
+    def _check_cacheless_inputs(self, q, k, v) -> None:
+        # The reference's checks (attention_backend.py:1586-1600), then the
+        # layout the store and prefill kernels take.
+        if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
+            raise ValueError("cacheless attention expects rank-3 Q/K/V")
+        if k.shape != v.shape:
+            raise ValueError("cacheless key and value shapes must match")
+        if q.size(0) != k.size(0):
+            raise ValueError("cacheless warmup requires matching query and KV token counts")
+        if q.size(1) % k.size(1):
+            raise ValueError("query head count must be divisible by KV head count")
+        if q.shape[1:] != (self.num_q_heads, self.head_dim) or k.shape[1:] != (self.num_kv_heads, self.head_dim):
+            raise ValueError("cacheless Q/K/V must have the backend's head counts and head_dim")
+        for t in (q, k, v):
+            if not t.is_cuda or t.dtype != self.dtype or t.stride(2) != 1:
+                raise ValueError("cacheless Q/K/V must be CUDA tensors of the backend dtype, unit inner stride")
+
+    def _run_warmup(self, q, k, v, common, output) -> None:
+        """Cacheless causal varlen attention (the WARMUP route) on the gfx950
+        kernels: the batch's K/V rows are stored into a temporary page pool
+        with the slot_mapping store kernel, then the ragged prefill kernel
+        runs with every sequence's keys equal to its queries.  Replaces the
+        reference's per-sequence SDPA fallback (attention_backend.py:1556-1624),
+        so memory profiling sees the serving kernels.  Like the reference, this
+        one-time path reads the query offsets to the host."""
+        device = q.device
+        bounds = np.asarray(common.query_start_loc.cpu().tolist(), dtype=np.int64)
+        q_lens = bounds[1:] - bounds[:-1]
+        if q.size(0) == 0 or q_lens.size == 0:
+            return
+        if np.any(q_lens < 0) or bounds[0] != 0 or bounds[-1] != q.size(0):
+            raise ValueError("cacheless query_start_loc must run from 0 to the token count")
+        counts = np.maximum((q_lens + PAGE_SIZE - 1) // PAGE_SIZE, 1)
+        first_page = np.cumsum(counts) - counts
+        seq_of = np.repeat(np.arange(q_lens.size), q_lens)
+        within = np.arange(q.size(0)) - np.repeat(bounds[:-1], q_lens)
+        slots = (first_page[seq_of] + within // PAGE_SIZE) * PAGE_SIZE + within % PAGE_SIZE
+        table = np.full((q_lens.size, int(counts.max())), -1, dtype=np.int64)
+        for s_idx, (base, c) in enumerate(zip(first_page, counts)):
+            table[s_idx, :c] = np.arange(base, base + c)
+        tile = ops.PREFILL_ROWS // (self.num_q_heads // self.num_kv_heads)
+        items = make_prefill_items(q_lens, q_lens, tile)
+        host = np.concatenate([slots, table.reshape(-1), q_lens, items.reshape(-1)]).astype(np.int32)
+        flat = _to_device(host, device)
+        n_slot, n_table = slots.size, table.size
+        slot_mapping = flat[:n_slot]
+        block_tables = flat[n_slot:n_slot + n_table].view(table.shape)
+        seq_lens = flat[n_slot + n_table:n_slot + n_table + q_lens.size]
+        prefill_items = flat[n_slot + n_table + q_lens.size:].view(items.shape)
+        pool = torch.empty((2, int(counts.sum()), PAGE_SIZE, self.num_kv_heads, self.head_dim), dtype=self.dtype,
+                           device=device)
+        ops.store_kvcache(k, v, pool[0], pool[1], slot_mapping)
+        ops.paged_prefill(q, pool[0], pool[1], block_tables, seq_lens, common.query_start_loc, prefill_items,
+                          items.shape[0], output, self.softmax_scale)
 
     def _run_prefill(self, q, k_cache, v_cache, common, metadata: MI355XAttentionMetadata, output) -> None:
         ops.paged_prefill(

@@ -146,3 +146,31 @@ def test_cacheless_warmup_route(gpu):
     empty = torch.empty(0, device=gpu)
     out = backend.forward(q.to(gpu), k.to(gpu), v.to(gpu), empty, empty, plan)
     assert_attention_close(out, ragged_attention(q, k, v, lengths))
+
+
+@pytest.mark.parametrize("lengths,hq,hkv", [([1, 15, 16, 17, 300], 32, 8), ([2049, 5], 16, 4), ([64], 8, 8), ([33, 1, 1], 16, 1)])
+def test_cacheless_warmup_runs_the_prefill_kernel(gpu, lengths, hq, hkv):
+    from my_vllm_amd.context import CommonAttentionMetadata
+
+    g = torch.Generator().manual_seed(sum(lengths) + hq)
+    total = sum(lengths)
+    q = torch.randn(total, hq, 128, generator=g).bfloat16()
+    kv = torch.randn(total, 2 * hkv, 128, generator=g).bfloat16()  # packed k|v: strided views
+    k, v = kv[:, :hkv], kv[:, hkv:]
+    qsl = [0]
+    for n in lengths:
+        qsl.append(qsl[-1] + n)
+    common = CommonAttentionMetadata(
+        num_prefill_seqs=len(lengths), num_decode_seqs=0, num_prefill_tokens=total, num_decode_tokens=0,
+        query_start_loc=torch.tensor(qsl, dtype=torch.int32, device=gpu),
+        seq_lens=torch.tensor(lengths, dtype=torch.int32, device=gpu),
+        slot_mapping=torch.full((total,), -1, dtype=torch.int32, device=gpu),
+        block_tables=None, max_q_len=max(lengths), max_kv_len=max(lengths), trusted=True)
+    backend = MI355XAttentionBackend(hq, hkv, 128, 16, torch.bfloat16)
+    plan = backend.build_plan(common)
+    assert plan.route is AttentionRoute.WARMUP
+    empty = torch.empty(0, device=gpu)
+    kvd = kv.to(gpu)
+    out = backend.forward(q.to(gpu), kvd[:, :hkv], kvd[:, hkv:], empty, empty, plan)
+    assert out.data_ptr() == backend._get_reusable_attention_output(q.to(gpu)).data_ptr()
+    assert_attention_close(out, ragged_attention(q, k.contiguous(), v.contiguous(), lengths))
