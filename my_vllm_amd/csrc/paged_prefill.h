@@ -26,7 +26,8 @@
 // the vector ALUs run the softmax of S(t), then accumulates P(t) V(t).  K runs
 // one tile ahead of V, so iteration t needs K(t+1) and V(t) resident while
 // K(t+2) and V(t+1) stream in.  The running max is only moved when it grows
-// by more than 8 (log2 units), so the O rescale is skipped on most tiles.
+// by more than 8 (log2 units), so P stays <= 2^8 and most tiles rescale O by
+// exactly 1.
 #pragma once
 
 #include "mva_common.h"
@@ -179,7 +180,6 @@ __device__ __attribute__((always_inline)) inline void prefill_item(
   float l = 0.f;
 
   // Softmax of S(t): P fragments for the PV k-steps and the O rescale factor.
-  // Returns whether any lane must rescale O before P(t) V(t) accumulates.
   auto softmax = [&](int tile, f32x16 (&st)[2], V8 (&pf)[4], float& alpha, auto masked_tag) {
     constexpr bool masked = decltype(masked_tag)::value;
     const int j0 = tile * kPrefillKeys;
@@ -211,7 +211,6 @@ __device__ __attribute__((always_inline)) inline void prefill_item(
         // PV k-step kk = 2*mt + (i/4)/2, slot (i/4 % 2)*4 + i%4.
         pf[2 * mt + ((i >> 2) >> 1)][((i >> 2) & 1) * 4 + (i & 3)] = (T)pr;
       }
-    return __any(grow);
   };
 
   // PV: A = V^T via transposed LDS reads.  16-lane group a = lane/16 covers
@@ -279,10 +278,11 @@ __device__ __attribute__((always_inline)) inline void prefill_item(
     qk(kb_next, st_next);
     V8 pf[4];
     float alpha;
-    if (softmax(t, st_cur, pf, alpha, masked_tag)) {
+    // Unconditional: alpha is exactly 1 on rows whose max did not move, and a
+    // branch on __any(grow) here makes the compiler keep two copies of O.
+    softmax(t, st_cur, pf, alpha, masked_tag);
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
-    }
+    for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
     pv(vb_cur, pf);
     st_cur[0] = st_next[0];
     st_cur[1] = st_next[1];
