@@ -235,6 +235,15 @@ def extra_measurements(device, steps: int):
         empty = q.new_empty((0, hkv, 128))
         return time_launches(lambda i: backend.forward(q, empty, empty, kc, vc, plan), iters, 3)
 
+    # Context for the MFMA-bound figures: the vendor library's dense bf16 GEMM
+    # on N(0,1) operands.  The chip holds lower clocks under dense MFMA work
+    # on real data than the 2.5 PFLOP/s peak assumes.
+    ga = _randn_rows(8192, 8192, seed=30, device=device, rng_device="cuda")
+    gb = _randn_rows(8192, 8192, seed=31, device=device, rng_device="cuda")
+    ms = time_launches(lambda i: torch.matmul(ga, gb), 30, 5)
+    res["gemm_8192_bf16_TFLOPs"] = round(2 * 8192**3 / ms / 1e9, 1)
+    del ga, gb
+
     # PURE_PREFILL with prefix, Qwen3-8B.
     batch = config_prefill(seed=2, device=device, rng_device="cuda")
     ms = attn_case(batch, 32, 8)

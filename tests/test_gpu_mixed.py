@@ -6,7 +6,7 @@ different split-K partition than the single launch's claims), so decode
 rows agree within the attention tolerance.  Both are checked against the
 fp32 oracle (2e-2 / 1e-2).
 The split route writes ``out[:P]`` and ``out[P:]`` of one buffer without
-concatenation.
+concatenation.  GQA ratios 1, 3 and 8 and fp16 run on both routes.
 """
 
 import pytest
@@ -56,3 +56,22 @@ def test_qwen3_8b_mixed_configuration(gpu):
     seqs = [0, 1, 2, 3, 4, 100, 259]
     exp, rows = expected(batch, seqs)
     assert_attention_close(out.cpu()[rows], exp)
+
+
+@pytest.mark.parametrize("mode", ["unified", "split"])
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (12, 4), (64, 8)])
+def test_mixed_gqa_ratios(gpu, mode, hq, hkv):
+    # G = 1, 3 and 8: the prefill tile of one launch holds 128 // G tokens of
+    # every query head of a KV head; decode wavefronts cover G heads each.
+    batch = make_paged_batch(97, [70, 33, 1, 1, 1], [70, 290, 9, 700, 2100], 2, hq, hkv)
+    out, plan = run_backend(batch, gpu, mode=mode)
+    assert plan.batch_type is BatchType.MIXED
+    assert_attention_close(out, expected(batch))
+
+
+@pytest.mark.parametrize("mode", ["unified", "split"])
+def test_mixed_fp16(gpu, mode):
+    batch = make_paged_batch(101, [40, 1, 1], [57, 333, 1200], 1, 32, 8, dtype=torch.float16)
+    out, _ = run_backend(batch, gpu, dtype=torch.float16, mode=mode)
+    assert out.dtype == torch.float16
+    assert_attention_close(out, expected(batch))
