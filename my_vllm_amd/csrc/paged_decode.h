@@ -281,8 +281,14 @@ static_assert((kDecodeClaimCounters + 1) * kDecodeSchedLineInts * 4 <= kDecodeSc
 //
 // A split piece stores its partial when it ends; decode_merge_wave combines
 // the partials in the kernel that follows on the same stream.
+//
+// `progress` (LDS, one int per wavefront of an 8-wavefront workgroup, or
+// nullptr): wavefronts w and w ^ 4 share a SIMD and stream the same pages for
+// two KV heads.  The older of the two wins issue arbitration and would finish
+// first; each wavefront publishes its page count and keeps priority 2 unless
+// it is ahead of its partner, so the pair stays level.
 template <typename T>
-__device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
+__device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds, int* progress = nullptr) {
   typedef typename Elem<T>::v8 V8;
   typedef typename Elem<T>::v4 V4;
   const int lane = threadIdx.x & 63;
@@ -477,7 +483,16 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds) {
 
   int i = 0;  // page of X being computed
   int buf = 0;
+  const int slot = (int)(threadIdx.x >> 6) & 7;
+  int steps = 0;
   for (;;) {
+    if (progress) {
+      if (lane == 0) progress[slot] = steps;
+      ++steps;
+      const int partner = __builtin_amdgcn_readfirstlane(*(volatile int*)&progress[slot ^ 4]);
+      if (partner >= steps) __builtin_amdgcn_s_setprio(2);
+      else __builtin_amdgcn_s_setprio(0);
+    }
     // Loop state is wave-uniform; re-assert it so that the lane-dependent
     // code in the loop does not make the compiler keep it in VGPRs.
     i = __builtin_amdgcn_readfirstlane(i);

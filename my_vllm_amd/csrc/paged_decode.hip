@@ -12,10 +12,14 @@ template <typename T, int kWaves>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_kernel(
     DecodeParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kWaves * kDecodeWaveLdsBytes];
+  // Page counts of the wavefronts (8-wavefront groups pair w with w ^ 4 on a
+  // SIMD); a wavefront without work reads as far ahead.
+  __shared__ int progress[8];
   const int w = kWaves == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int wave = (int)blockIdx.x * kWaves + w;
+  if (kWaves == 8 && (threadIdx.x & 63) == 0) progress[w] = 0x3fffffff;
   if (wave >= p.num_waves) return;
-  decode_wave<T>(p, wave, (lds_u8*)lds + w * kDecodeWaveLdsBytes);
+  decode_wave<T>(p, wave, (lds_u8*)lds + w * kDecodeWaveLdsBytes, kWaves == 8 ? progress : nullptr);
 }
 
 template <typename T>
