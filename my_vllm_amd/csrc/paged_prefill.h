@@ -26,8 +26,8 @@
 // the vector ALUs run the softmax of S(t), then accumulates P(t) V(t).  K runs
 // one tile ahead of V, so iteration t needs K(t+1) and V(t) resident while
 // K(t+2) and V(t+1) stream in.  The running max is only moved when it grows
-// by more than 8 (log2 units), so P stays <= 2^8 and most tiles rescale O by
-// exactly 1.
+// by more than 8 (log2 units), so P stays <= 2^8 and the O rescale is skipped
+// on most tiles.
 #pragma once
 
 #include "mva_common.h"
@@ -255,13 +255,14 @@ __device__ __attribute__((always_inline)) inline void prefill_item(
   }
   __builtin_amdgcn_s_waitcnt(kVmcnt0);
   __syncthreads();
-  f32x16 st_cur[2];
-  qk(k0, st_cur);
+  f32x16 st_a[2], st_b[2];  // S(t) lives in st_a for even t, st_b for odd t
+  qk(k0, st_a);
 
   // Iteration t.  kb_cur holds K(t) (free: S(t) is done) and receives
-  // K(t+2); kb_next holds K(t+1); vb_cur holds V(t); vb_next receives V(t+1).
+  // K(t+2); kb_next holds K(t+1); vb_cur holds V(t); vb_next receives V(t+1);
+  // st_cur holds S(t) and st_next receives S(t+1).
   auto iteration = [&](int t, lds_u8* kb_cur, lds_u8* kb_next, lds_u8* vb_cur, lds_u8* vb_next,
-                       auto masked_tag) {
+                       f32x16 (&st_cur)[2], f32x16 (&st_next)[2], auto masked_tag) {
     __builtin_amdgcn_s_waitcnt(kVmcnt0);
     __syncthreads();  // K(t+1), V(t) landed for all waves; S(t) and PV(t-1) done everywhere
     if (t == ntiles - 1 && (t + 1) * kPrefillKeys > kv) {
@@ -274,29 +275,30 @@ __device__ __attribute__((always_inline)) inline void prefill_item(
     pg_k = page_of(t + 3);
     // S(t+1) on the matrix cores alongside the softmax of S(t).  Past the
     // last tile this reads a stale buffer and the result is never used.
-    f32x16 st_next[2];
     qk(kb_next, st_next);
     V8 pf[4];
     float alpha;
-    // Unconditional: alpha is exactly 1 on rows whose max did not move, and a
-    // branch on __any(grow) here makes the compiler keep two copies of O.
     softmax(t, st_cur, pf, alpha, masked_tag);
+    // alpha is exactly 1 on rows whose max did not move: most tiles skip the
+    // rescale.  (With S(t) and S(t+1) in fixed registers the branch leaves O
+    // in place; a copy of S per tile made the compiler keep two copies of O.)
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+      for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+    }
     pv(vb_cur, pf);
-    st_cur[0] = st_next[0];
-    st_cur[1] = st_next[1];
   };
 
   // Tiles below every row's causal bound, then the masked diagonal tiles.
-  // Unrolled by two so each iteration body names its LDS buffers statically.
+  // Unrolled by two so each iteration body names its LDS buffers and S
+  // registers statically.
   auto run = [&](int t, int t_stop, auto masked_tag) {
-    if (t < t_stop && (t & 1)) iteration(t++, k1, k0, v1, v0, masked_tag);
+    if (t < t_stop && (t & 1)) iteration(t++, k1, k0, v1, v0, st_b, st_a, masked_tag);
     for (; t + 1 < t_stop; t += 2) {
-      iteration(t, k0, k1, v0, v1, masked_tag);
-      iteration(t + 1, k1, k0, v1, v0, masked_tag);
+      iteration(t, k0, k1, v0, v1, st_a, st_b, masked_tag);
+      iteration(t + 1, k1, k0, v1, v0, st_b, st_a, masked_tag);
     }
-    if (t < t_stop) iteration(t, k0, k1, v0, v1, masked_tag);
+    if (t < t_stop) iteration(t, k0, k1, v0, v1, st_a, st_b, masked_tag);
   };
   run(0, full_tiles, std::false_type{});
   run(full_tiles, ntiles, std::true_type{});
