@@ -112,6 +112,8 @@ _SIGNATURES = {
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+# The C ABI revision these signatures describe (mva_abi_version()).
+ABI_VERSION = 4
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -141,6 +143,13 @@ def load_library() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.restype = restype
             fn.argtypes = argtypes
+        revision = lib.mva_abi_version()
+        if revision != ABI_VERSION:
+            _load_error = RuntimeError(f"ABI revision {revision}")
+            raise RuntimeError(
+                f"{LIB_PATH} has C ABI revision {revision}, this package expects {ABI_VERSION}; "
+                "rebuild it with `python -m my_vllm_amd.build`"
+            )
         _lib = lib
         return lib
 

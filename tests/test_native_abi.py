@@ -35,7 +35,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     lib = _native.load_library()
     for name in _declared_functions():
         assert hasattr(lib, name), f"{name} missing from {_native.LIB_PATH.name}"
-    assert lib.mva_abi_version() == 4
+    assert lib.mva_abi_version() == 4 == _native.ABI_VERSION
 
 
 def test_library_binds_to_the_process_hip_runtime():
@@ -81,3 +81,12 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     with pytest.raises(RuntimeError, match="missing"):
         _native.load_library()
     assert _native.native_available() is False
+
+
+def test_abi_revision_mismatch_raises(monkeypatch):
+    # A library built from other sources than this package's signatures
+    # describe must not load.
+    monkeypatch.setattr(_native, "_lib", None)
+    monkeypatch.setattr(_native, "ABI_VERSION", _native.ABI_VERSION + 1)
+    with pytest.raises(RuntimeError, match="ABI revision"):
+        _native.load_library()
