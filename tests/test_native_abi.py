@@ -87,6 +87,7 @@ def test_abi_revision_mismatch_raises(monkeypatch):
     # A library built from other sources than this package's signatures
     # describe must not load.
     monkeypatch.setattr(_native, "_lib", None)
+    monkeypatch.setattr(_native, "_load_error", _native._load_error)
     monkeypatch.setattr(_native, "ABI_VERSION", _native.ABI_VERSION + 1)
     with pytest.raises(RuntimeError, match="ABI revision"):
         _native.load_library()
