@@ -112,9 +112,10 @@ def headline(args, device):
     empty = q.new_empty((0, hkv, 128))
 
     def step(i):
+        # Attention.forward's store + attention, as the layer calls it: the
+        # backend folds the store into the piece-list decode launch.
         kc, vc = caches[i % copies]
-        store(k_new, v_new, kc, vc, common.slot_mapping)
-        backend.forward(q, empty, empty, kc, vc, plan)
+        backend.forward_with_kv_store(q, k_new, v_new, kc, vc, common.slot_mapping, plan, store)
 
     torch.cuda.synchronize()
     ms_step = time_launches(step, args.steps, args.warmup)

@@ -180,6 +180,34 @@ int mva_paged_decode(const void* q, int64_t q_token_stride, int64_t q_head_strid
                      int page_size, float softmax_scale, int dtype, void* stream);
 
 /*
+ * mva_paged_decode with the slot_mapping KV store of the same step folded in
+ * (piece lists only: wave_extra is required).  Before reading any page, the
+ * wavefront whose piece holds the last page of a sequence writes the new
+ * K and V rows of that piece's KV head, k_new / v_new
+ * [num_new_tokens, num_kv_heads, 128] (row q_row of the piece, any 4-byte
+ * aligned strides), to cache slot slot_mapping[q_row] (int32, or int64 when
+ * slot_is_int64; -1 skips).  The slot must lie in the sequence's last page,
+ * as the model runner builds it; then the output and the caches equal
+ * mva_kv_store followed by mva_paged_decode.  Other arguments as
+ * mva_paged_decode.
+ * Replaces the KVCacheStore call (nanovllm/layers/attention.py:140-141)
+ * together with the decode run that follows it (attention_backend.py:995-997).
+ */
+int mva_paged_decode_store(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                           const void* k_cache, const void* v_cache, int64_t num_pages,
+                           int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
+                           int64_t block_table_stride, const int32_t* seq_lens, const int32_t* items,
+                           int64_t num_items, int64_t num_waves, const int32_t* wave_extra,
+                           int waves_per_group, const int32_t* merges, int64_t num_merges,
+                           int64_t num_part_slots, void* out, int64_t out_token_stride,
+                           int64_t out_head_stride, void* workspace, int64_t workspace_bytes,
+                           const void* k_new, int64_t k_token_stride, int64_t k_head_stride,
+                           const void* v_new, int64_t v_token_stride, int64_t v_head_stride,
+                           const void* slot_mapping, int slot_is_int64, int64_t num_new_tokens,
+                           int num_q_heads, int num_kv_heads, int head_dim, int page_size,
+                           float softmax_scale, int dtype, void* stream);
+
+/*
  * Fixed-shape variant of mva_paged_decode for capture in a HIP graph: every
  * argument that changes from one decode step to the next lives in device
  * memory at a fixed address, so one captured launch serves every step whose

@@ -88,5 +88,10 @@ class Attention(nn.Module):
             raise RuntimeError("attention metadata and plan must be prepared before forward")
         k_cache, v_cache = self.k_cache, self.v_cache
         if k_cache.numel() and v_cache.numel():
+            fused = getattr(self.backend, "forward_with_kv_store", None)
+            if fused is not None:
+                # The MI355X backend folds the store into a piece-list decode
+                # launch and otherwise runs self.kv_store first.
+                return fused(q, k, v, k_cache, v_cache, metadata.slot_mapping, plan, self.kv_store)
             self.kv_store(k, v, k_cache, v_cache, metadata.slot_mapping)
         return self.backend.forward(q, k, v, k_cache, v_cache, plan)

@@ -640,6 +640,9 @@ class MI355XAttentionBackendMixin:
         self._output_buffer: torch.Tensor | None = None
         self._workspace: torch.Tensor | None = None
         self._active_graph_state: MI355XFullDecodeGraphState | None = None
+        # (key, value, slot_mapping) of the step while forward_with_kv_store
+        # folds the KV store into the decode launch.
+        self._pending_store: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None
 
     # ---- capability contract -------------------------------------------------
     @classmethod
@@ -884,6 +887,37 @@ class MI355XAttentionBackendMixin:
         if k_cache.shape != v_cache.shape or k_cache.stride() != v_cache.stride():
             raise ValueError("key and value caches must share shape and layout")
 
+    def forward_with_kv_store(self, q, k, v, k_cache, v_cache, slot_mapping, plan, store=None) -> torch.Tensor:
+        """The KV store of ``Attention.forward`` (``attention.py:140-141``) followed by
+        :meth:`forward`, as one call.
+
+        A DECODE step planned with piece lists writes the new rows inside the
+        decode launch (``mva_paged_decode_store``): the result and the caches
+        are those of the store followed by the decode.  Every other step runs
+        ``store`` (the layer's ``KVCacheStore``; the HIP store when None) and
+        then :meth:`forward`.
+        """
+        metadata = plan.metadata if isinstance(plan, AttentionPlan) else None
+        if (
+            self._active_graph_state is None
+            and isinstance(metadata, MI355XAttentionMetadata)
+            and plan.route is self.route_type.DECODE
+            and metadata.decode_wave_extra is not None
+            and _has_cache(k_cache)
+            and _has_cache(v_cache)
+            and k is not None
+            and v is not None
+            and k.dim() == 3
+            and k.size(0) == q.size(0)
+        ):
+            self._pending_store = (k, v, slot_mapping)
+            try:
+                return self.forward(q, k, v, k_cache, v_cache, plan)
+            finally:
+                self._pending_store = None
+        (store if store is not None else ops.store_kvcache)(k, v, k_cache, v_cache, slot_mapping)
+        return self.forward(q, k, v, k_cache, v_cache, plan)
+
     def forward(self, q, k, v, k_cache, v_cache, plan) -> torch.Tensor:
         metadata = _require_plan_metadata(plan, MI355XAttentionMetadata, self.backend_name, self.plan_type)
         Route = self.route_type
@@ -951,6 +985,17 @@ class MI355XAttentionBackendMixin:
         group = self.num_q_heads // self.num_kv_heads
         ws_bytes = ops.decode_workspace_bytes(metadata.num_decode_part_slots, self.num_kv_heads, group)
         workspace = self._get_workspace(ws_bytes, q.device)
+        if self._pending_store is not None:
+            key, value, slot_mapping = self._pending_store
+            ops.paged_decode_store(
+                q, key, value, slot_mapping, k_cache, v_cache,
+                metadata.block_tables, metadata.seq_lens,
+                metadata.decode_items, metadata.num_decode_items, metadata.num_decode_waves,
+                metadata.decode_merges, metadata.num_decode_merges, metadata.num_decode_part_slots,
+                output, workspace, self.softmax_scale,
+                metadata.decode_wave_extra, metadata.decode_waves_per_group,
+            )
+            return
         ops.paged_decode(
             q,
             k_cache,

@@ -92,6 +92,19 @@ struct DecodeParams {
   // and the merge grid then hold capacities).  nullptr: the scalars above.
   const int32_t* counts;
   int32_t* sched;  // claim counters and exit counter, see kDecodeClaimCounters
+  // Fused slot_mapping store (piece lists), or k_new == nullptr: before its
+  // first page, a wavefront writes the new K/V row of (token q_row, KV head)
+  // to cache slot slots[q_row] for every piece of its list that holds the
+  // sequence's last page (that piece is the only reader of the row).
+  const void* k_new;
+  int64_t kn_tok_stride;
+  int64_t kn_head_stride;
+  const void* v_new;
+  int64_t vn_tok_stride;
+  int64_t vn_head_stride;
+  const void* slots;
+  int slots_int64;
+  int num_new;  // rows of k_new / v_new / slots
   void* out;
   int64_t out_tok_stride;
   int64_t out_head_stride;
@@ -355,6 +368,29 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds, int* p
     const T* qp = q_addr(X);
 #pragma unroll
     for (int j = 0; j < 4; ++j) qf[j] = ld16<u32x4>(qp + 8 * j);
+  }
+  // Fused store: the new token's K and V rows (256 bytes each, 4 per lane)
+  // of every listed piece that reads its sequence's last page, loaded while
+  // the page table and queries are in flight and written before any page
+  // is read (the wait below also retires the stores).
+  if (listed && p.k_new) {
+    const int first = max(sload(p.wave_extra, wave), 0);
+    const int count = min(sload(p.wave_extra, wave + 1), N) - first;
+    for (int k = -1; k < count; ++k) {
+      const i32x8 d = k < 0 ? X : desc_at(first + k);
+      const int len = sload(p.seq_lens, d[0]);
+      if (d[6] < 0 || d[6] >= p.num_new || len <= 0 || d[1] * kPageSize >= len || d[2] * kPageSize < len) continue;
+      const int64_t slot = p.slots_int64 ? ((const int64_t*)p.slots)[d[6]] : ((const int32_t*)p.slots)[d[6]];
+      if (slot < 0 || slot / kPageSize >= p.num_pages) continue;
+      const int64_t dst = (slot / kPageSize) * p.page_stride + (slot % kPageSize) * p.tok_stride +
+                          (int64_t)d[7] * kHeadDim + 2 * lane;
+      const uint32_t kv = *(const uint32_t*)((const T*)p.k_new + (int64_t)d[6] * p.kn_tok_stride +
+                                            (int64_t)d[7] * p.kn_head_stride + 2 * lane);
+      const uint32_t vv = *(const uint32_t*)((const T*)p.v_new + (int64_t)d[6] * p.vn_tok_stride +
+                                            (int64_t)d[7] * p.vn_head_stride + 2 * lane);
+      *(uint32_t*)((T*)const_cast<void*>(p.k_cache) + dst) = kv;
+      *(uint32_t*)((T*)const_cast<void*>(p.v_cache) + dst) = vv;
+    }
   }
   __builtin_amdgcn_s_waitcnt(kVmcnt0);
   DecodeStepIo io;

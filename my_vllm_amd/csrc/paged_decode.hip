@@ -125,6 +125,10 @@ int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, i
   p.out_tok_stride = out_token_stride;
   p.out_head_stride = out_head_stride;
   uint8_t* ws = (uint8_t*)workspace;
+  p.k_new = nullptr;
+  p.v_new = nullptr;
+  p.slots = nullptr;
+  p.num_new = 0;
   p.sched = (int32_t*)ws;
   ws += kDecodeSchedBytes;
   p.part_lse = (float*)ws;
@@ -166,6 +170,53 @@ extern "C" int mva_paged_decode(const void* q, int64_t q_token_stride, int64_t q
   if (wave_extra == nullptr && waves_per_group != 1)
     return set_error("paged attention: the claim schedule runs one wavefront per workgroup");
   if (num_items == 0) return 0;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == kBF16) rc = launch_paged_decode<__bf16>(p, waves_per_group, s);
+  else if (dtype == kF16) rc = launch_paged_decode<_Float16>(p, waves_per_group, s);
+  else return set_error("paged attention: dtype must be bf16 or fp16");
+  if (rc) return rc;
+  return launch_decode_merge(p, merges, num_merges, dtype, s);
+}
+
+extern "C" int mva_paged_decode_store(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                                      const void* k_cache, const void* v_cache, int64_t num_pages,
+                                      int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
+                                      int64_t block_table_stride, const int32_t* seq_lens,
+                                      const int32_t* items, int64_t num_items, int64_t num_waves,
+                                      const int32_t* wave_extra, int waves_per_group,
+                                      const int32_t* merges, int64_t num_merges,
+                                      int64_t num_part_slots, void* out, int64_t out_token_stride,
+                                      int64_t out_head_stride, void* workspace, int64_t workspace_bytes,
+                                      const void* k_new, int64_t k_token_stride, int64_t k_head_stride,
+                                      const void* v_new, int64_t v_token_stride, int64_t v_head_stride,
+                                      const void* slot_mapping, int slot_is_int64, int64_t num_new_tokens,
+                                      int num_q_heads, int num_kv_heads, int head_dim, int page_size,
+                                      float softmax_scale, int dtype, void* stream) {
+  using namespace mva;
+  if (wave_extra == nullptr) return set_error("paged attention: the fused store needs piece lists (wave_extra)");
+  if (k_new == nullptr || v_new == nullptr || slot_mapping == nullptr)
+    return set_error("paged attention: the fused store needs k, v and slot_mapping");
+  if (num_new_tokens < 0 || num_new_tokens > 0x7fffffffLL) return set_error("paged attention: invalid token count");
+  if (((uint64_t)(uintptr_t)k_new | (uint64_t)(uintptr_t)v_new | (uint64_t)(k_token_stride * 2) |
+       (uint64_t)(k_head_stride * 2) | (uint64_t)(v_token_stride * 2) | (uint64_t)(v_head_stride * 2)) % 4)
+    return set_error("paged attention: k / v rows must be 4-byte aligned");
+  DecodeParams p;
+  int rc = fill_decode_params(p, q, q_token_stride, q_head_stride, k_cache, v_cache, num_pages,
+                              page_stride, token_stride, block_tables, block_table_stride, seq_lens,
+                              items, num_items, num_waves, wave_extra, merges, num_merges, num_part_slots, out,
+                              out_token_stride, out_head_stride, workspace, workspace_bytes, num_q_heads,
+                              num_kv_heads, head_dim, page_size, softmax_scale);
+  if (rc) return rc;
+  if (num_items == 0) return 0;
+  p.k_new = k_new;
+  p.kn_tok_stride = k_token_stride;
+  p.kn_head_stride = k_head_stride;
+  p.v_new = v_new;
+  p.vn_tok_stride = v_token_stride;
+  p.vn_head_stride = v_head_stride;
+  p.slots = slot_mapping;
+  p.slots_int64 = slot_is_int64 ? 1 : 0;
+  p.num_new = (int)num_new_tokens;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == kBF16) rc = launch_paged_decode<__bf16>(p, waves_per_group, s);
   else if (dtype == kF16) rc = launch_paged_decode<_Float16>(p, waves_per_group, s);

@@ -388,6 +388,66 @@ def paged_decode(
     )
 
 
+def paged_decode_store(
+    q: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    items: torch.Tensor,
+    num_items: int,
+    num_waves: int,
+    merges: torch.Tensor | None,
+    num_merges: int,
+    num_part_slots: int,
+    out: torch.Tensor,
+    workspace: torch.Tensor | None,
+    softmax_scale: float,
+    wave_extra: torch.Tensor,
+    waves_per_group: int = 1,
+) -> None:
+    """:func:`store_kvcache` of this step's ``key``/``value`` and :func:`paged_decode`
+    in one launch (piece lists only).
+
+    Each new row lands in its sequence's last page, which only one piece per
+    KV head reads; that piece's wavefront writes the row before reading any
+    page.  ``key``/``value`` are ``[T, Hkv, D]`` with unit inner stride;
+    ``slot_mapping`` int32/int64 ``[T]`` (``< 0`` = skip).
+    """
+    num_q_heads, head_dim = q.shape[1], q.shape[2]
+    num_pages, page_size, num_kv_heads = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
+    num_tokens = key.shape[0]
+    if key.shape != value.shape or key.dim() != 3 or key.shape[1:] != (num_kv_heads, head_dim):
+        raise ValueError("key and value must be [T, num_kv_heads, head_dim]")
+    if key.dtype != q.dtype or value.dtype != q.dtype:
+        raise TypeError("key and value must have the query dtype")
+    if key.stride(-1) != 1 or value.stride(-1) != 1:
+        raise ValueError("key and value need unit stride in the last dimension")
+    if slot_mapping.numel() != num_tokens or slot_mapping.dtype not in (torch.int32, torch.int64):
+        raise ValueError("slot_mapping must be int32/int64 with one slot per token")
+    ws_ptr = workspace.data_ptr() if workspace is not None else 0
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _native.call(
+        "mva_paged_decode_store",
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k_cache.data_ptr(), v_cache.data_ptr(), num_pages, k_cache.stride(0), k_cache.stride(1),
+        block_tables.data_ptr(), block_tables.stride(0), seq_lens.data_ptr(),
+        items.data_ptr(), num_items, num_waves,
+        wave_extra.data_ptr(), int(waves_per_group),
+        merges.data_ptr() if merges is not None else 0, num_merges, num_part_slots,
+        out.data_ptr(), out.stride(0), out.stride(1),
+        ws_ptr, ws_bytes,
+        key.data_ptr(), key.stride(0), key.stride(1),
+        value.data_ptr(), value.stride(0), value.stride(1),
+        slot_mapping.data_ptr(), 1 if slot_mapping.dtype == torch.int64 else 0, num_tokens,
+        num_q_heads, num_kv_heads, head_dim, page_size, float(softmax_scale),
+        _native.dtype_code(q.dtype), _native.stream_handle(q.device),
+    )
+
+
 def paged_decode_graph(
     q: torch.Tensor,
     k_cache: torch.Tensor,

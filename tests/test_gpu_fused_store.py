@@ -1,0 +1,73 @@
+"""The slot_mapping KV store folded into the piece-list decode launch.
+
+``forward_with_kv_store`` on a DECODE step must leave the caches and the
+output bit-identical to ``store_kvcache`` followed by ``forward`` (the
+reference's ``Attention.forward`` order, nanovllm/layers/attention.py:131-143);
+the rows it stores are a bit copy, and the attention sees them because the
+only reader of each row writes it first.  Steps the fused launch does not
+cover (claim schedule, prefill) fall back to the separate store.
+"""
+
+import dataclasses
+
+import pytest
+import torch
+
+from my_vllm_amd import ops
+from my_vllm_amd.attention_backend import AttentionRoute, MI355XAttentionBackend
+from my_vllm_amd.workloads import config_decode_small, make_paged_batch
+from tests._util import assert_attention_close
+from tests.test_gpu_prefill import expected, to_device
+
+pytestmark = pytest.mark.gpu
+
+
+def _both_ways(batch, device, dtype=torch.bfloat16, slots=None):
+    hq, hkv = batch.q.shape[1], batch.k_cache.shape[2]
+    common, q, kc, vc = to_device(batch, device)
+    k_new, v_new = batch.k_new.to(device), batch.v_new.to(device)
+    slot_mapping = common.slot_mapping if slots is None else slots.to(device)
+    backend = MI355XAttentionBackend(hq, hkv, 128, 16, dtype)
+    plan = backend.build_plan(common)
+    kc_a, vc_a = kc.clone(), vc.clone()
+    ops.store_kvcache(k_new, v_new, kc_a, vc_a, slot_mapping)
+    sep = backend.forward(q, k_new, v_new, kc_a, vc_a, plan).clone()
+    kc_b, vc_b = kc.clone(), vc.clone()
+    fused = backend.forward_with_kv_store(q, k_new, v_new, kc_b, vc_b, slot_mapping, plan).clone()
+    return plan, sep, fused, (kc_a, vc_a), (kc_b, vc_b)
+
+
+def test_headline_decode_step_matches_store_then_decode(gpu):
+    batch = config_decode_small(seed=1)
+    plan, sep, fused, (kc_a, vc_a), (kc_b, vc_b) = _both_ways(batch, gpu)
+    assert plan.route is AttentionRoute.DECODE and plan.metadata.decode_wave_extra is not None
+    assert torch.equal(kc_a, kc_b) and torch.equal(vc_a, vc_b)
+    assert torch.equal(sep, fused)
+    seqs = [0, 1, 31, 63]
+    stored = dataclasses.replace(batch, k_cache=kc_a.cpu(), v_cache=vc_a.cpu())
+    exp, rows = expected(stored, seqs)
+    assert_attention_close(fused.cpu()[rows], exp)
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (12, 3), (8, 1)])
+def test_page_boundaries_int64_slots_and_skips(gpu, hq, hkv):
+    # New tokens at the first, last and a middle row of their page, one-page
+    # sequences, and a -1 slot that must leave the cache untouched.
+    ctx = [1, 16, 17, 32, 300, 513, 2049]
+    batch = make_paged_batch(83, [1] * len(ctx), ctx, 0, hq, hkv, dtype=torch.float16)
+    slots = batch.common.slot_mapping.to(torch.int64).clone()
+    slots[2] = -1
+    plan, sep, fused, (kc_a, vc_a), (kc_b, vc_b) = _both_ways(batch, gpu, torch.float16, slots)
+    assert torch.equal(kc_a, kc_b) and torch.equal(vc_a, vc_b)
+    assert torch.equal(sep, fused)
+
+
+def test_claim_schedule_falls_back_to_the_separate_store(gpu, monkeypatch):
+    monkeypatch.setenv("MVA_DECODE_SCHEDULE", "claims")
+    batch = make_paged_batch(89, [1] * 5, [40, 7, 1000, 16, 129], 0, 32, 8)
+    plan, sep, fused, (kc_a, vc_a), (kc_b, vc_b) = _both_ways(batch, gpu)
+    assert plan.metadata.decode_wave_extra is None
+    assert torch.equal(kc_a, kc_b) and torch.equal(vc_a, vc_b)
+    assert torch.equal(sep, fused)
+    stored = dataclasses.replace(batch, k_cache=kc_a.cpu(), v_cache=vc_a.cpu())
+    assert_attention_close(fused, expected(stored))

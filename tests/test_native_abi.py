@@ -35,7 +35,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     lib = _native.load_library()
     for name in _declared_functions():
         assert hasattr(lib, name), f"{name} missing from {_native.LIB_PATH.name}"
-    assert lib.mva_abi_version() == 4 == _native.ABI_VERSION
+    assert lib.mva_abi_version() == 5 == _native.ABI_VERSION
 
 
 def test_library_binds_to_the_process_hip_runtime():
