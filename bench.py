@@ -94,10 +94,10 @@ def causal_pairs(q_lens, kv_lens) -> int:
 
 def headline(args, device):
     from my_vllm_amd import ops
-    from my_vllm_amd.attention import KVCacheStore
+    from my_vllm_amd.layers import KVCacheStore
     from my_vllm_amd.attention_backend import MI355XAttentionBackend
     from my_vllm_amd.custom_op import CustomOpConfig
-    from my_vllm_amd.workloads import config_decode_small
+    from workloads import config_decode_small
 
     batch = config_decode_small(seed=1)
     hq, hkv = 16, 8
@@ -196,7 +196,7 @@ def cpu_baseline(batch, seconds: float):
 def extra_measurements(device, steps: int):
     from my_vllm_amd import ops
     from my_vllm_amd.attention_backend import MI355XAttentionBackend
-    from my_vllm_amd.workloads import config_long_decode, config_mixed, config_prefill, silu_input
+    from workloads import config_long_decode, config_mixed, config_prefill, silu_input
 
     res = {}
     # SiLU-and-mul, Qwen3-0.6B MLP: 8 rotating inputs (600 MB > Infinity Cache).
@@ -213,7 +213,7 @@ def extra_measurements(device, steps: int):
 
     # RMSNorm and fused residual-add RMSNorm, 4096 tokens x 4096 (Qwen3-8B
     # hidden), 8 rotating inputs (the residual pair: 512 MB > Infinity Cache).
-    from my_vllm_amd.workloads import silu_input as _randn_rows
+    from workloads import silu_input as _randn_rows
 
     xs = [_randn_rows(4096, 4096, seed=10 + i, device=device, rng_device="cuda") for i in range(8)]
     rs = [_randn_rows(4096, 4096, seed=20 + i, device=device, rng_device="cuda") for i in range(8)]
@@ -287,8 +287,8 @@ def prologue_fused_vs_separate(device, tokens: int = 4096, hq: int = 32, hkv: in
     RMSNorm + RoPE + KV store as one launch vs the four separate ops."""
     from my_vllm_amd import ops
     from my_vllm_amd.custom_op import CustomOpConfig
-    from my_vllm_amd.rotary_embedding import RotaryEmbedding
-    from my_vllm_amd.workloads import silu_input as _randn_rows
+    from my_vllm_amd.layers import RotaryEmbedding
+    from workloads import silu_input as _randn_rows
 
     width = (hq + 2 * hkv) * 128
     qkv = _randn_rows(tokens, width, seed=30, device=device, rng_device="cuda")
@@ -324,10 +324,10 @@ def graph_vs_eager(device, batch_size: int = 8, ctx: int = 512, steps: int = 200
     """Launch-bound decode step (KV store + attention) for a small batch at the
     Qwen3-0.6B shape: eager launches vs one replay of a captured HIP graph of
     the same two launches, per step (plan built once, as in steady decode)."""
-    from my_vllm_amd.attention import KVCacheStore
+    from my_vllm_amd.layers import KVCacheStore
     from my_vllm_amd.attention_backend import MI355XAttentionBackend
     from my_vllm_amd.custom_op import CustomOpConfig
-    from my_vllm_amd.workloads import make_paged_batch
+    from workloads import make_paged_batch
 
     hq, hkv = 16, 8
     batch = make_paged_batch(7, [1] * batch_size, [ctx] * batch_size, 0, hq, hkv)
@@ -381,7 +381,7 @@ def run_only(args, device):
     """One workload's kernel, --steps launches, for rocprofv3 passes."""
     from my_vllm_amd import ops
     from my_vllm_amd.attention_backend import MI355XAttentionBackend
-    from my_vllm_amd.workloads import (config_decode_small, config_long_decode, config_mixed, config_prefill,
+    from workloads import (config_decode_small, config_long_decode, config_mixed, config_prefill,
                                        silu_input)
 
     n = args.steps

@@ -130,6 +130,11 @@ int mva_qk_norm_rope_store(const void* q_in, void* q_out, int64_t q_token_stride
  */
 int64_t mva_decode_workspace_bytes(int64_t num_part_slots, int num_kv_heads, int group);
 
+/* Byte offset, inside a decode workspace, of the int32 word that
+ * mva_paged_decode_store sets when a new row's slot is not in its sequence's
+ * last page. */
+#define MVA_DECODE_STORE_ERROR_OFFSET 4224
+
 /*
  * Paged GQA decode (one query token per sequence) over an NHD page cache
  * k_cache / v_cache = [num_pages, page_size, num_kv_heads, head_dim] with
@@ -188,7 +193,10 @@ int mva_paged_decode(const void* q, int64_t q_token_stride, int64_t q_head_strid
  * aligned strides), to cache slot slot_mapping[q_row] (int32, or int64 when
  * slot_is_int64; -1 skips).  The slot must lie in the sequence's last page,
  * as the model runner builds it; then the output and the caches equal
- * mva_kv_store followed by mva_paged_decode.  Other arguments as
+ * mva_kv_store followed by mva_paged_decode.  A row whose slot lies in any
+ * other page is not written (another wavefront may be reading that page):
+ * the launch sets the int32 word at byte MVA_DECODE_STORE_ERROR_OFFSET of the
+ * workspace to 1, and only the caller clears it.  Other arguments as
  * mva_paged_decode.
  * Replaces the KVCacheStore call (nanovllm/layers/attention.py:140-141)
  * together with the decode run that follows it (attention_backend.py:995-997).

@@ -156,17 +156,29 @@ def load_library() -> ctypes.CDLL:
         except OSError as error:
             _load_error = error
             raise RuntimeError(f"cannot load {LIB_PATH}: {error}") from error
+        rebuild = "rebuild it with `python -m my_vllm_amd.build`"
+        # The revision first: a stale library may lack entry points added
+        # since, and that must read as "rebuild", not as a missing attribute.
+        try:
+            version_fn = lib.mva_abi_version
+        except AttributeError:
+            _load_error = RuntimeError("no mva_abi_version")
+            raise RuntimeError(f"{LIB_PATH} exports no mva_abi_version; {rebuild}") from None
+        version_fn.restype, version_fn.argtypes = ctypes.c_int, []
+        revision = version_fn()
+        if revision != ABI_VERSION:
+            _load_error = RuntimeError(f"ABI revision {revision}")
+            raise RuntimeError(
+                f"{LIB_PATH} has C ABI revision {revision}, this package expects {ABI_VERSION}; {rebuild}"
+            )
+        missing = [name for name in _SIGNATURES if not hasattr(lib, name)]
+        if missing:
+            _load_error = RuntimeError(f"missing exports {missing}")
+            raise RuntimeError(f"{LIB_PATH} lacks the entry points {', '.join(missing)}; {rebuild}")
         for name, (restype, argtypes) in _SIGNATURES.items():
             fn = getattr(lib, name)
             fn.restype = restype
             fn.argtypes = argtypes
-        revision = lib.mva_abi_version()
-        if revision != ABI_VERSION:
-            _load_error = RuntimeError(f"ABI revision {revision}")
-            raise RuntimeError(
-                f"{LIB_PATH} has C ABI revision {revision}, this package expects {ABI_VERSION}; "
-                "rebuild it with `python -m my_vllm_amd.build`"
-            )
         _lib = lib
         return lib
 

@@ -1,17 +1,10 @@
-"""Attention backend lifecycle, registry and the MI355X (gfx950) backend.
+"""The MI355X (gfx950) attention backend.
 
-The first half restates the reference's backend-neutral contract
-(nanovllm/layers/attention_backend.py): ``AttentionRoute`` (:112-117),
-``AttentionPlan`` (:120-135), the ``AttentionBackend`` lifecycle (:174-275),
-``AttentionBackendRegistry`` (:1228-1381), metadata validation (:1384-1481),
-batch classification (:1484-1491) and the cacheless warmup fallback
-(:1556-1624).
-
-The second half is the new backend.  ``MI355XAttentionBackendMixin`` holds the
-whole implementation and takes the plan/route/batch-type classes from class
-attributes, so the same code can subclass either this module's
-``AttentionBackend`` (``MI355XAttentionBackend`` below) or the reference's own
-``AttentionBackend`` and be registered in the reference's registry unchanged.
+``MI355XAttentionBackendMixin`` holds the whole implementation and takes the
+plan/route/batch-type/metadata classes from class attributes, so the same code
+runs on this package's contract classes (``MI355XAttentionBackend``) or on the
+reference's own (``integrate`` builds those subclasses and registers them in
+the reference's ``AttentionBackendRegistry``).
 
 Per step: ``build_metadata`` turns the trusted host ints of
 ``CommonAttentionMetadata`` into device work lists (no device reads),
@@ -19,7 +12,7 @@ Per step: ``build_metadata`` turns the trusted host ints of
 launches the gfx950 kernels on the current stream into a reusable,
 backend-owned output buffer:
 
-* DECODE        -> paged GQA decode (split-K + in-launch LSE merge)
+* DECODE        -> paged GQA decode (piece lists or claims, split-K merge kernel)
 * PREFILL       -> ragged causal chunked prefill over prefix-cached pages
 * MIXED_UNIFIED -> one launch writing ``out[:P]`` (prefill) and ``out[P:]`` (decode)
 * MIXED_SPLIT   -> prefill launch into ``out[:P]`` + decode launch into ``out[P:]``
@@ -30,191 +23,23 @@ from __future__ import annotations
 
 import os
 from dataclasses import dataclass
-from enum import Enum
-from math import sqrt
 from types import MappingProxyType
 from typing import Any
 
 import numpy as np
 import torch
-import torch.nn.functional as F
 
 from . import _native, ops
-from .context import BatchType, CommonAttentionMetadata
-
-
-class AttentionRoute(str, Enum):
-    WARMUP = "warmup"
-    PREFILL = "prefill"
-    DECODE = "decode"
-    MIXED_UNIFIED = "mixed_unified"
-    MIXED_SPLIT = "mixed_split"
-
-
-@dataclass(frozen=True)
-class AttentionPlan:
-    """One explicit, backend-owned execution decision for a scheduled batch."""
-
-    batch_type: BatchType
-    route: AttentionRoute
-    common: CommonAttentionMetadata
-    metadata: Any
-
-    @property
-    def common_metadata(self) -> CommonAttentionMetadata:
-        return self.common
-
-    @property
-    def backend_metadata(self) -> Any:
-        return self.metadata
-
-
-class AttentionBackend:
-    """Unified lifecycle implemented by every complete attention backend."""
-
-    backend_name = "base"
-    supports_full_decode_graph = False
-
-    def __init__(
-        self,
-        num_q_heads: int,
-        num_kv_heads: int,
-        head_dim: int,
-        block_size: int,
-        dtype: torch.dtype,
-    ) -> None:
-        if num_q_heads <= 0 or num_kv_heads <= 0:
-            raise ValueError("attention head counts must be positive")
-        if num_q_heads % num_kv_heads:
-            raise ValueError("num_q_heads must be divisible by num_kv_heads")
-        if head_dim <= 0 or block_size <= 0:
-            raise ValueError("head_dim and block_size must be positive")
-        self.num_q_heads = num_q_heads
-        self.num_kv_heads = num_kv_heads
-        self.head_dim = head_dim
-        self.block_size = block_size
-        self.dtype = dtype
-        self.softmax_scale = 1.0 / sqrt(head_dim)
-
-    @classmethod
-    def support_reason(cls, *, block_size: int, dtype: torch.dtype, device=None, **_: Any) -> str | None:
-        del block_size, dtype, device
-        return None
-
-    @classmethod
-    def supports(cls, **capabilities: Any) -> bool:
-        return cls.support_reason(**capabilities) is None
-
-    def build_metadata(self, common: CommonAttentionMetadata) -> Any:
-        raise NotImplementedError
-
-    def build_plan(self, common: CommonAttentionMetadata, metadata: Any | None = None) -> AttentionPlan:
-        raise NotImplementedError
-
-    def forward(self, q, k, v, k_cache, v_cache, plan: AttentionPlan) -> torch.Tensor:
-        raise NotImplementedError
-
-    def create_full_decode_graph_state(self, batch_size: int, page_indices_capacity: int, device) -> Any:
-        raise RuntimeError(f"{type(self).__name__} does not support full decode CUDA Graph")
-
-    def full_decode_graph_metadata_fits(self, state: Any, plan: AttentionPlan) -> bool:
-        del state, plan
-        return False
-
-    def plan_full_decode_graph(self, state: Any, plan: AttentionPlan) -> None:
-        raise RuntimeError(f"{type(self).__name__} does not support full decode CUDA Graph")
-
-    def activate_full_decode_graph(self, state: Any) -> None:
-        raise RuntimeError(f"{type(self).__name__} does not support full decode CUDA Graph")
-
-    def deactivate_full_decode_graph(self) -> None:
-        return None
-
-
-# --------------------------------------------------------------------------
-# Shared validation helpers (nanovllm/layers/attention_backend.py:1384-1553).
-# --------------------------------------------------------------------------
-
-def _validate_common_metadata(common: Any, *, require_cuda: bool, common_type=CommonAttentionMetadata) -> None:
-    if not isinstance(common, common_type):
-        raise TypeError("common must be CommonAttentionMetadata")
-    for name in (
-        "num_prefill_seqs",
-        "num_decode_seqs",
-        "num_prefill_tokens",
-        "num_decode_tokens",
-        "max_q_len",
-        "max_kv_len",
-        "num_kv_blocks",
-        "num_prefill_kv_blocks",
-    ):
-        value = getattr(common, name)
-        if isinstance(value, bool) or not isinstance(value, int):
-            raise TypeError(f"common.{name} must be an int")
-        if value < 0:
-            raise ValueError(f"common.{name} must be non-negative")
-    if common.num_seqs <= 0:
-        raise ValueError("attention metadata must contain at least one sequence")
-    if common.num_decode_tokens != common.num_decode_seqs:
-        raise ValueError("decode suffix must contain one query token per sequence")
-    if not isinstance(common.trusted, bool):
-        raise TypeError("common.trusted must be a bool")
-    for name in ("query_start_loc", "seq_lens", "slot_mapping"):
-        tensor = getattr(common, name)
-        if not isinstance(tensor, torch.Tensor):
-            raise TypeError(f"common.{name} must be a torch.Tensor")
-        if tensor.dtype != torch.int32:
-            raise TypeError(f"common.{name} must have dtype torch.int32")
-        if tensor.ndim != 1:
-            raise ValueError(f"common.{name} must be one-dimensional")
-        if require_cuda and tensor.device.type != "cuda":
-            raise ValueError(f"common.{name} must be on CUDA")
-    if common.query_start_loc.numel() != common.num_seqs + 1:
-        raise ValueError("query_start_loc length must equal number of sequences + 1")
-    if common.seq_lens.numel() != common.num_seqs:
-        raise ValueError("seq_lens length must equal number of sequences")
-    if common.slot_mapping.numel() != common.num_query_tokens:
-        raise ValueError("slot_mapping length must equal number of query tokens")
-    if not common.trusted:
-        if int(common.query_start_loc[0].item()) != 0:
-            raise ValueError("query_start_loc must start at zero")
-        if int(common.query_start_loc[-1].item()) != common.num_query_tokens:
-            raise ValueError("query_start_loc must end at num_query_tokens")
-        query_lengths = common.query_start_loc[1:] - common.query_start_loc[:-1]
-        if common.num_decode_seqs and not bool(torch.all(query_lengths[common.num_prefill_seqs:] == 1).item()):
-            raise ValueError("every decode sequence must have one query token")
-        if not bool(torch.all(common.seq_lens > 0).item()):
-            raise ValueError("all KV sequence lengths must be positive")
-    block_tables = common.block_tables
-    if block_tables is not None:
-        if not isinstance(block_tables, torch.Tensor):
-            raise TypeError("common.block_tables must be a torch.Tensor")
-        if block_tables.dtype != torch.int32:
-            raise TypeError("common.block_tables must have dtype torch.int32")
-        if block_tables.ndim != 2:
-            raise ValueError("common.block_tables must be two-dimensional")
-        if block_tables.size(0) != common.num_seqs:
-            raise ValueError("block_tables row count must equal number of sequences")
-        if require_cuda and block_tables.device.type != "cuda":
-            raise ValueError("common.block_tables must be on CUDA")
-
-
-def _classify_batch(common: Any, batch_type_enum=BatchType):
-    if common.num_prefill_seqs == 0:
-        if common.num_decode_seqs <= 0:
-            raise ValueError("pure decode batch must contain decode requests")
-        return batch_type_enum.PURE_DECODE
-    if common.num_decode_seqs == 0:
-        return batch_type_enum.PURE_PREFILL
-    return batch_type_enum.MIXED
-
-
-def _require_plan_metadata(plan: Any, metadata_type: type, backend_name: str, plan_type=AttentionPlan):
-    if not isinstance(plan, plan_type):
-        raise TypeError("attention forward requires AttentionPlan")
-    if not isinstance(plan.metadata, metadata_type):
-        raise TypeError(f"{backend_name} plan carries incompatible backend metadata")
-    return plan.metadata
+from .contract import (
+    AttentionBackend,
+    AttentionPlan,
+    AttentionRoute,
+    BatchType,
+    CommonAttentionMetadata,
+    check_common_metadata,
+    classify_batch,
+    plan_metadata,
+)
 
 
 def _has_cache(cache: torch.Tensor | None) -> bool:
@@ -695,7 +520,7 @@ class MI355XAttentionBackendMixin:
 
     # ---- per-step metadata and plan ------------------------------------------
     def build_metadata(self, common) -> MI355XAttentionMetadata:
-        _validate_common_metadata(common, require_cuda=self.require_device_metadata, common_type=self.common_type)
+        check_common_metadata(common, require_cuda=self.require_device_metadata, common_type=self.common_type)
         if common.block_tables is None:
             return MI355XAttentionMetadata(
                 query_start_loc=common.query_start_loc,
@@ -827,7 +652,7 @@ class MI355XAttentionBackendMixin:
         Route = self.route_type
         Batch = self.batch_type_enum
         # The single phase classification point for the whole batch.
-        batch_type = _classify_batch(common, Batch)
+        batch_type = classify_batch(common, Batch)
         if metadata.is_cacheless:
             route = Route.WARMUP
         elif batch_type is Batch.PURE_PREFILL:
@@ -891,16 +716,18 @@ class MI355XAttentionBackendMixin:
         """The KV store of ``Attention.forward`` (``attention.py:140-141``) followed by
         :meth:`forward`, as one call.
 
-        A DECODE step planned with piece lists writes the new rows inside the
-        decode launch (``mva_paged_decode_store``): the result and the caches
-        are those of the store followed by the decode.  Every other step runs
-        ``store`` (the layer's ``KVCacheStore``; the HIP store when None) and
-        then :meth:`forward`.
+        A DECODE step of trusted metadata (the model runner's, whose slots
+        lie in each sequence's last page) planned with piece lists writes the
+        new rows inside the decode launch (``mva_paged_decode_store``): the
+        result and the caches are those of the store followed by the decode.
+        Every other step runs ``store`` (the layer's ``KVCacheStore``; the
+        HIP store when None) and then :meth:`forward`.
         """
-        metadata = plan.metadata if isinstance(plan, AttentionPlan) else None
+        metadata = plan.metadata if isinstance(plan, self.plan_type) else None
         if (
             self._active_graph_state is None
             and isinstance(metadata, MI355XAttentionMetadata)
+            and getattr(plan.common, "trusted", False) is True
             and plan.route is self.route_type.DECODE
             and metadata.decode_wave_extra is not None
             and _has_cache(k_cache)
@@ -919,7 +746,7 @@ class MI355XAttentionBackendMixin:
         return self.forward(q, k, v, k_cache, v_cache, plan)
 
     def forward(self, q, k, v, k_cache, v_cache, plan) -> torch.Tensor:
-        metadata = _require_plan_metadata(plan, MI355XAttentionMetadata, self.backend_name, self.plan_type)
+        metadata = plan_metadata(plan, MI355XAttentionMetadata, self.backend_name, self.plan_type)
         Route = self.route_type
         Batch = self.batch_type_enum
         has_k_cache = _has_cache(k_cache)
@@ -1014,6 +841,13 @@ class MI355XAttentionBackendMixin:
             metadata.decode_wave_extra,
             metadata.decode_waves_per_group,
         )
+
+    def fused_store_error(self) -> bool:
+        """Whether a folded decode store since the last call skipped a row
+        whose slot was not in its sequence's last page (reads the device)."""
+        if self._workspace is None:
+            return False
+        return ops.decode_store_error(self._workspace)
 
     def _run_decode_graph(self, q, k_cache, v_cache, state: MI355XFullDecodeGraphState) -> None:
         counts, items, wave_extra, merges = state.views()
@@ -1233,114 +1067,37 @@ class MI355XSplitAttentionBackend(MI355XAttentionBackend):
     default_attention_mode = "split"
 
 
-class AttentionBackendRegistry:
-    """Registry of complete attention backends (reference :1228-1381 semantics).
+def integrate(registry: Any, base: type, plan_type: type, route_type: type, batch_type_enum: type,
+              common_type: type, names: tuple[str, str] = ("mi355x", "mi355x_split")) -> tuple[type, type]:
+    """Build the backend on another contract's classes and register it.
 
-    ``create("auto", ...)`` selects the MI355X backend when it supports the
-    requested capabilities.  Unlike the reference, ``attention_mode`` is passed
-    to every registered backend whose constructor accepts it.
+    ``base`` is that contract's ``AttentionBackend`` (the reference's:
+    nanovllm/layers/attention_backend.py:174-275) and the four types its
+    plan, route, batch-type and metadata classes.  Two classes are
+    registered under ``names``: MIXED batches in one launch, and MIXED as
+    prefill + decode launches (the reference's registry passes
+    ``attention_mode`` to FlashInfer only, attention_backend.py:1376-1381, so
+    the mode is carried by the name).  Returns ``(unified, split)``.
     """
-
-    _BACKENDS: dict[str, type[AttentionBackend]] = {
-        "mi355x": MI355XAttentionBackend,
-        "mi355x_split": MI355XSplitAttentionBackend,
-    }
-    _ALIASES: dict[str, str] = {"hip": "mi355x", "gfx950": "mi355x"}
-
-    @classmethod
-    def registered_names(cls) -> tuple[str, ...]:
-        return tuple(cls._BACKENDS)
-
-    @classmethod
-    def names(cls) -> tuple[str, ...]:
-        return cls.registered_names()
-
-    @classmethod
-    def register(cls, name: str, backend_type: type[AttentionBackend]) -> None:
-        if not isinstance(name, str):
-            raise TypeError("attention backend name must be a string")
-        normalized = name.strip().lower()
-        if not normalized or normalized == "auto":
-            raise ValueError("attention backend name must be non-empty and not 'auto'")
-        if normalized in cls._BACKENDS or normalized in cls._ALIASES:
-            raise ValueError(f"attention backend name {normalized!r} is already registered")
-        if not isinstance(backend_type, type) or not issubclass(backend_type, AttentionBackend):
-            raise TypeError("backend_type must be an AttentionBackend subclass")
-        cls._BACKENDS[normalized] = backend_type
-
-    @staticmethod
-    def _support_status(backend_type: type[AttentionBackend], capabilities: dict[str, Any]):
-        supported = backend_type.supports(**capabilities)
-        if type(supported) is not bool:
-            raise TypeError(f"{backend_type.__name__}.supports() must return a bool")
-        if supported:
-            return True, None
-        reason = backend_type.support_reason(**capabilities)
-        if reason is not None and not isinstance(reason, str):
-            raise TypeError(f"{backend_type.__name__}.support_reason() must return a string or None")
-        return False, reason or "supports() returned False"
-
-    @classmethod
-    def create(
-        cls,
-        name: str = "auto",
-        *,
-        num_q_heads: int,
-        num_kv_heads: int,
-        head_dim: int,
-        block_size: int,
-        dtype: torch.dtype,
-        attention_mode: str = "unified",
-        device: torch.device | str | None = None,
-    ) -> AttentionBackend:
-        if not isinstance(name, str):
-            raise TypeError("attention backend name must be a string")
-        requested = name.strip().lower()
-        canonical = cls._ALIASES.get(requested, requested)
-        capabilities = {
-            "num_q_heads": num_q_heads,
-            "num_kv_heads": num_kv_heads,
-            "head_dim": head_dim,
-            "block_size": block_size,
-            "dtype": dtype,
-            "device": device,
-            "attention_mode": attention_mode,
-        }
-        init_kwargs = {
-            "num_q_heads": num_q_heads,
-            "num_kv_heads": num_kv_heads,
-            "head_dim": head_dim,
-            "block_size": block_size,
-            "dtype": dtype,
-        }
-        if canonical == "auto":
-            supported, reason = cls._support_status(MI355XAttentionBackend, capabilities)
-            if supported:
-                return MI355XAttentionBackend(**init_kwargs, attention_mode=attention_mode)
-            raise RuntimeError(f"No usable attention backend. mi355x: {reason}")
-        backend_type = cls._BACKENDS.get(canonical)
-        if backend_type is None:
-            supported_names = ", ".join(("auto", *cls.registered_names()))
-            raise ValueError(f"unknown attention backend {name!r}; choose from {supported_names}")
-        supported, reason = cls._support_status(backend_type, capabilities)
-        if not supported:
-            raise RuntimeError(f"{canonical} attention backend is unusable: {reason}")
-        if issubclass(backend_type, MI355XAttentionBackendMixin):
-            mode = "split" if backend_type.default_attention_mode == "split" else attention_mode
-            return backend_type(**init_kwargs, attention_mode=mode)
-        return backend_type(**init_kwargs)
+    family = {"plan_type": plan_type, "route_type": route_type, "batch_type_enum": batch_type_enum,
+              "common_type": common_type}
+    unified = type("MI355XBackend", (MI355XAttentionBackendMixin, base),
+                   {"__module__": __name__, "backend_name": names[0], **family})
+    split = type("MI355XSplitBackend", (unified,),
+                 {"__module__": __name__, "backend_name": names[1], "default_attention_mode": "split"})
+    registry.register(names[0], unified)
+    registry.register(names[1], split)
+    return unified, split
 
 
 __all__ = [
-    "AttentionBackend",
-    "AttentionBackendRegistry",
-    "AttentionPlan",
-    "AttentionRoute",
     "MI355XAttentionBackend",
     "MI355XAttentionBackendMixin",
     "MI355XAttentionMetadata",
     "MI355XSplitAttentionBackend",
+    "integrate",
     "make_decode_plan",
+    "make_decode_plan_listed",
     "make_prefill_items",
     "resident_decode_waves",
 ]

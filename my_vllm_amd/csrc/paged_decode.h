@@ -273,6 +273,11 @@ constexpr int kDecodeClaimCounters = 32;
 constexpr int kDecodeSchedLineInts = 32;
 constexpr int kDecodeSchedBytes = 4352;  // (32 + 1) lines of 128 bytes, rounded up to 256
 static_assert((kDecodeClaimCounters + 1) * kDecodeSchedLineInts * 4 <= kDecodeSchedBytes, "sched area");
+// Word set to 1 by a fused-store launch that found a new row whose slot is
+// not in its sequence's last page (the row is not written); on its own line
+// after the exit counter.  Only the host clears it.
+constexpr int kDecodeStoreErrorInt = (kDecodeClaimCounters + 1) * kDecodeSchedLineInts;
+static_assert((kDecodeStoreErrorInt + 1) * 4 <= kDecodeSchedBytes, "store error word");
 
 // One wavefront of a decode launch (`wave` in [0, num_waves)); `lds` is its
 // kDecodeWaveLdsBytes of LDS.
@@ -381,7 +386,16 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds, int* p
       const int len = sload(p.seq_lens, d[0]);
       if (d[6] < 0 || d[6] >= p.num_new || len <= 0 || d[1] * kPageSize >= len || d[2] * kPageSize < len) continue;
       const int64_t slot = p.slots_int64 ? ((const int64_t*)p.slots)[d[6]] : ((const int32_t*)p.slots)[d[6]];
-      if (slot < 0 || slot / kPageSize >= p.num_pages) continue;
+      if (slot < 0) continue;  // -1: nothing to store
+      // The row must land in the sequence's last page, which this piece
+      // alone reads; a slot anywhere else could be a page another wavefront
+      // is streaming.  Such a row is not written, and the launch records it
+      // in the workspace's store-error word.
+      const int last_page = sload(p.block_tables, (int64_t)d[0] * p.bt_stride + (len - 1) / kPageSize);
+      if (slot / kPageSize != last_page || slot / kPageSize >= p.num_pages) {
+        if (lane == 0) *(volatile int32_t*)(p.sched + kDecodeStoreErrorInt) = 1;
+        continue;
+      }
       const int64_t dst = (slot / kPageSize) * p.page_stride + (slot % kPageSize) * p.tok_stride +
                           (int64_t)d[7] * kHeadDim + 2 * lane;
       const uint32_t kv = *(const uint32_t*)((const T*)p.k_new + (int64_t)d[6] * p.kn_tok_stride +

@@ -1,10 +1,18 @@
-"""Construction-time dispatch for ordinary operators (mirror of the reference).
+"""Construction-time dispatch for ordinary operators.
 
-Restates nanovllm/layers/custom_op.py:16-120: an immutable per-op override
-map, platform detection, and a ``CustomOp`` base class that binds
-``forward_<platform>`` once in ``__init__`` so the forward hot path does no
-dispatch.  On ROCm PyTorch the device type is ``"cuda"``, so ``forward_cuda``
-is the method bound on MI355X.
+Interface of the reference's nanovllm/layers/custom_op.py:16-120, which the
+model's layers are written against:
+
+* ``CustomOpConfig(platform, dtype, overrides)``: frozen; the platform and
+  every override value are lower-cased, the override map is read-only and
+  detached from the caller's dict; ``implementation_for(op)`` defaults to
+  ``"auto"``; the config is hashable (it keys shared-module caches);
+* ``CustomOp``: an ``nn.Module`` whose ``forward`` is bound once, at
+  construction, to ``forward_<platform>`` (``dispatch_forward``), falling back
+  to ``forward_native``; on ROCm PyTorch the platform is ``"cuda"``.
+
+This package's operators (``layers.py``) implement only ``forward_cuda`` and
+take their kernels from the provider table in ``providers.py``.
 """
 
 from __future__ import annotations
@@ -17,7 +25,12 @@ from typing import Any, Callable
 import torch
 from torch import nn
 
-_NATIVE_IMPLEMENTATIONS = frozenset({"native", "native_torch"})
+PLATFORMS = ("auto", "cuda", "cpu", "xpu")
+NATIVE_IMPLEMENTATIONS = frozenset({"native", "native_torch"})
+
+
+def _lowered_copy(overrides: Mapping[str, str]) -> Mapping[str, str]:
+    return MappingProxyType({str(op): str(choice).lower() for op, choice in overrides.items()})
 
 
 @dataclass(frozen=True)
@@ -30,25 +43,22 @@ class CustomOpConfig:
 
     def __post_init__(self) -> None:
         platform = self.platform.lower()
-        if platform not in ("auto", "cuda", "cpu", "xpu"):
+        if platform not in PLATFORMS:
             raise ValueError("platform must be 'auto', 'cuda', 'cpu', or 'xpu'")
-        normalized = {
-            str(operator): str(implementation).lower()
-            for operator, implementation in self.overrides.items()
-        }
         object.__setattr__(self, "platform", platform)
-        object.__setattr__(self, "overrides", MappingProxyType(normalized))
+        object.__setattr__(self, "overrides", _lowered_copy(self.overrides))
 
     def implementation_for(self, operator: str) -> str:
         return self.overrides.get(operator, "auto")
 
     def __hash__(self) -> int:
-        return hash((self.platform, self.dtype, tuple(sorted(self.overrides.items()))))
+        return hash((self.platform, self.dtype, frozenset(self.overrides.items())))
 
 
-def _detect_platform() -> str:
-    device = torch.device(torch.get_default_device())
-    return device.type if device.type in ("cuda", "cpu", "xpu") else "cpu"
+def default_platform() -> str:
+    """The device type new tensors land on, or "cpu" for any other device type."""
+    kind = torch.get_default_device().type
+    return kind if kind in PLATFORMS[1:] else "cpu"
 
 
 class CustomOp(nn.Module):
@@ -58,9 +68,9 @@ class CustomOp(nn.Module):
 
     def __init__(self, custom_op_config: CustomOpConfig | None = None) -> None:
         super().__init__()
-        self.custom_op_config = custom_op_config or CustomOpConfig()
-        configured = self.custom_op_config.platform
-        self.platform = _detect_platform() if configured == "auto" else configured
+        config = custom_op_config if custom_op_config is not None else CustomOpConfig()
+        self.custom_op_config = config
+        self.platform = default_platform() if config.platform == "auto" else config.platform
         self._forward_method = self.dispatch_forward()
 
     @property
@@ -68,10 +78,7 @@ class CustomOp(nn.Module):
         return self.custom_op_config.implementation_for(self.op_name)
 
     def dispatch_forward(self) -> Callable[..., Any]:
-        method = getattr(self, f"forward_{self.platform}", None)
-        if method is None:
-            return self.forward_native
-        return method
+        return getattr(self, "forward_" + self.platform, self.forward_native)
 
     def forward(self, *args: Any, **kwargs: Any) -> Any:
         return self._forward_method(*args, **kwargs)
@@ -89,13 +96,13 @@ class CustomOp(nn.Module):
         return self.forward_native(*args, **kwargs)
 
     def require_cuda_implementation(self, supported: set[str] | frozenset[str]) -> str:
-        implementation = self.requested_implementation
-        if implementation not in supported:
-            available = ", ".join(sorted(supported))
-            raise ValueError(
-                f"unsupported {self.op_name!r} implementation "
-                f"{implementation!r}; available: {available}"
-            )
-        if self.platform != "cuda" and implementation not in ("auto", *_NATIVE_IMPLEMENTATIONS):
-            raise RuntimeError(f"{implementation!r} for {self.op_name!r} requires CUDA")
-        return implementation
+        """The requested provider name of this op, after the reference's two
+        checks: it must be one of ``supported`` (ValueError), and only "auto"
+        and the native names may be asked for off CUDA (RuntimeError)."""
+        choice = self.requested_implementation
+        if choice not in supported:
+            names = ", ".join(sorted(supported))
+            raise ValueError(f"unsupported {self.op_name!r} implementation {choice!r}; available: {names}")
+        if self.platform != "cuda" and choice != "auto" and choice not in NATIVE_IMPLEMENTATIONS:
+            raise RuntimeError(f"{choice!r} for {self.op_name!r} requires CUDA")
+        return choice

@@ -330,6 +330,22 @@ def decode_workspace_bytes(num_part_slots: int, num_kv_heads: int, group: int) -
     return nbytes
 
 
+# Byte offset of the fused store's error word in a decode workspace
+# (MVA_DECODE_STORE_ERROR_OFFSET in include/my_vllm_amd.h).
+DECODE_STORE_ERROR_OFFSET = 4224
+
+
+def decode_store_error(workspace: torch.Tensor, clear: bool = True) -> bool:
+    """Whether a :func:`paged_decode_store` launch on ``workspace`` met a row
+    whose slot is not in its sequence's last page (and skipped it).  Reads
+    the device, so it synchronizes with the stream; ``clear`` resets the word."""
+    word = workspace[DECODE_STORE_ERROR_OFFSET:DECODE_STORE_ERROR_OFFSET + 4].view(torch.int32)
+    flagged = bool(word.item() != 0)
+    if flagged and clear:
+        word.zero_()
+    return flagged
+
+
 def decode_merge_list(items):
     """The merge entries of a decode plan: chunk 0 of every split segment.
 
@@ -414,12 +430,19 @@ def paged_decode_store(
 
     Each new row lands in its sequence's last page, which only one piece per
     KV head reads; that piece's wavefront writes the row before reading any
-    page.  ``key``/``value`` are ``[T, Hkv, D]`` with unit inner stride;
-    ``slot_mapping`` int32/int64 ``[T]`` (``< 0`` = skip).
+    page.  A row whose slot is in another page is not written and sets the
+    workspace word at :data:`DECODE_STORE_ERROR_OFFSET` (see
+    :func:`decode_store_error`).  ``key``/``value`` are ``[T, Hkv, D]`` with
+    unit inner stride; ``slot_mapping`` int32/int64 ``[T]`` (``< 0`` = skip).
     """
     num_q_heads, head_dim = q.shape[1], q.shape[2]
     num_pages, page_size, num_kv_heads = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
     num_tokens = key.shape[0]
+    # The kernel dereferences these pointers: they must be device memory on
+    # the query's GPU (as store_kvcache requires).
+    for name, t in (("key", key), ("value", value), ("slot_mapping", slot_mapping)):
+        if not t.is_cuda or t.device != q.device:
+            raise RuntimeError(f"paged_decode_store expects {name} as a CUDA tensor on the query's device")
     if key.shape != value.shape or key.dim() != 3 or key.shape[1:] != (num_kv_heads, head_dim):
         raise ValueError("key and value must be [T, num_kv_heads, head_dim]")
     if key.dtype != q.dtype or value.dtype != q.dtype:

@@ -14,15 +14,13 @@ import numpy as np
 
 from my_vllm_amd import ops
 from my_vllm_amd.attention_backend import (
-    AttentionBackendRegistry,
-    AttentionRoute,
     MI355XAttentionBackend,
     _to_device,
     make_decode_plan,
     make_decode_plan_listed,
 )
-from my_vllm_amd.context import BatchType
-from my_vllm_amd.workloads import config_decode_small, decode_lengths, make_paged_batch
+from my_vllm_amd.contract import AttentionRoute, BatchType
+from workloads import config_decode_small, decode_lengths, make_paged_batch
 from oracle.reference import paged_attention
 from tests._util import assert_attention_close
 
@@ -225,7 +223,7 @@ def test_one_key_context_returns_v_exactly(gpu):
     assert torch.equal(out.cpu(), expected)
 
 
-def test_registry_creates_backend(gpu):
-    backend = AttentionBackendRegistry.create("auto", num_q_heads=16, num_kv_heads=8, head_dim=128,
-                                              block_size=16, dtype=torch.bfloat16)
-    assert isinstance(backend, MI355XAttentionBackend)
+def test_backend_supports_this_gpu(gpu):
+    caps = dict(num_q_heads=16, num_kv_heads=8, head_dim=128, block_size=16, dtype=torch.bfloat16, device=gpu)
+    assert MI355XAttentionBackend.support_reason(**caps) is None
+    assert MI355XAttentionBackend.supports(**caps) is True

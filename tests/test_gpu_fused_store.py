@@ -14,8 +14,9 @@ import pytest
 import torch
 
 from my_vllm_amd import ops
-from my_vllm_amd.attention_backend import AttentionRoute, MI355XAttentionBackend
-from my_vllm_amd.workloads import config_decode_small, make_paged_batch
+from my_vllm_amd.attention_backend import MI355XAttentionBackend
+from my_vllm_amd.contract import AttentionRoute
+from workloads import config_decode_small, make_paged_batch
 from tests._util import assert_attention_close
 from tests.test_gpu_prefill import expected, to_device
 

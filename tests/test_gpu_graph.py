@@ -10,9 +10,10 @@ path, with eager work and synchronizations between replays.
 import pytest
 import torch
 
-from my_vllm_amd.attention_backend import AttentionRoute, MI355XAttentionBackend
-from my_vllm_amd.context import CommonAttentionMetadata
-from my_vllm_amd.workloads import decode_lengths, make_paged_batch
+from my_vllm_amd.attention_backend import MI355XAttentionBackend
+from my_vllm_amd.contract import AttentionRoute
+from my_vllm_amd.contract import CommonAttentionMetadata
+from workloads import decode_lengths, make_paged_batch
 from oracle.reference import paged_attention
 from tests._util import assert_attention_close
 

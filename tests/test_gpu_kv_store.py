@@ -5,7 +5,7 @@ import pytest
 import torch
 
 from my_vllm_amd import ops
-from my_vllm_amd.attention import KVCacheStore
+from my_vllm_amd.layers import KVCacheStore
 from my_vllm_amd.custom_op import CustomOpConfig
 from oracle.reference import kv_store
 

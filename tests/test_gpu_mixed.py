@@ -12,9 +12,9 @@ concatenation.  GQA ratios 1, 3 and 8 and fp16 run on both routes.
 import pytest
 import torch
 
-from my_vllm_amd.attention_backend import AttentionRoute
-from my_vllm_amd.context import BatchType
-from my_vllm_amd.workloads import config_mixed, make_paged_batch
+from my_vllm_amd.contract import AttentionRoute
+from my_vllm_amd.contract import BatchType
+from workloads import config_mixed, make_paged_batch
 from tests._util import assert_attention_close
 from tests.test_gpu_prefill import expected, run_backend
 

@@ -10,9 +10,10 @@ stale rows, fp16, trusted vs untrusted metadata, and the cacheless warmup.
 import pytest
 import torch
 
-from my_vllm_amd.attention_backend import AttentionRoute, MI355XAttentionBackend
-from my_vllm_amd.context import BatchType
-from my_vllm_amd.workloads import config_prefill, make_paged_batch
+from my_vllm_amd.attention_backend import MI355XAttentionBackend
+from my_vllm_amd.contract import AttentionRoute
+from my_vllm_amd.contract import BatchType
+from workloads import config_prefill, make_paged_batch
 from oracle.reference import paged_attention, ragged_attention
 from tests._util import assert_attention_close
 
@@ -132,7 +133,7 @@ def test_cacheless_warmup_route(gpu):
     q = torch.randn(4, 16, 128).bfloat16()
     k = torch.randn(4, 4, 128).bfloat16()
     v = torch.randn(4, 4, 128).bfloat16()
-    from my_vllm_amd.context import CommonAttentionMetadata
+    from my_vllm_amd.contract import CommonAttentionMetadata
 
     common = CommonAttentionMetadata(
         num_prefill_seqs=2, num_decode_seqs=0, num_prefill_tokens=4, num_decode_tokens=0,
@@ -150,7 +151,7 @@ def test_cacheless_warmup_route(gpu):
 
 @pytest.mark.parametrize("lengths,hq,hkv", [([1, 15, 16, 17, 300], 32, 8), ([2049, 5], 16, 4), ([64], 8, 8), ([33, 1, 1], 16, 1)])
 def test_cacheless_warmup_runs_the_prefill_kernel(gpu, lengths, hq, hkv):
-    from my_vllm_amd.context import CommonAttentionMetadata
+    from my_vllm_amd.contract import CommonAttentionMetadata
 
     g = torch.Generator().manual_seed(sum(lengths) + hq)
     total = sum(lengths)

@@ -17,7 +17,7 @@ import torch
 
 from my_vllm_amd import ops
 from my_vllm_amd.custom_op import CustomOpConfig
-from my_vllm_amd.layernorm import RMSNorm
+from my_vllm_amd.layers import RMSNorm
 from oracle.reference import fused_add_rms_norm, rms_norm, rms_scaled
 from tests._util import max_ulp_diff
 
@@ -104,9 +104,6 @@ def test_custom_op_providers(gpu):
     _, exp_res = fused_add_rms_norm(x, r, w, 1e-6)
     assert torch.equal(res.cpu(), exp_res)
     assert_rms_matches(out, x.float() + r.float(), w, 1e-6)
-    native = RMSNorm(1024, 1e-6, CustomOpConfig(platform="cuda", overrides={"rms_norm": "native",
-                                                                            "fused_add_rms_norm": "native"}))
-    assert native.rms_provider_name == "native_torch"
     alias = RMSNorm(1024, 1e-6, CustomOpConfig(platform="cuda", overrides={"rms_norm": "flashinfer"}))
     assert alias.rms_provider_name == "hip"
     with pytest.raises(RuntimeError, match="CUDA tensor"):

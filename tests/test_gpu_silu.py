@@ -4,9 +4,9 @@ import pytest
 import torch
 
 from my_vllm_amd import ops
-from my_vllm_amd.activation import SiluAndMul
+from my_vllm_amd.layers import SiluAndMul
 from my_vllm_amd.custom_op import CustomOpConfig
-from my_vllm_amd.workloads import silu_input
+from workloads import silu_input
 from oracle.reference import silu_and_mul_eager, silu_and_mul_fused
 from tests._util import max_ulp_diff
 
@@ -59,10 +59,11 @@ def test_silu_rejects_unsupported_inputs(gpu, make, pattern):
         ops.silu_and_mul(make(gpu))
 
 
-@pytest.mark.parametrize("override", ["auto", "hip", "custom_cuda"])
+@pytest.mark.parametrize("override", ["auto", "hip", "custom_cuda", "adaptive_cuda", "flashinfer"])
 def test_custom_op_selects_gfx950_kernel(gpu, override):
+    # The reference's provider names all select the gfx950 kernel.
     layer = SiluAndMul(CustomOpConfig(platform="cuda", dtype=torch.bfloat16, overrides={"silu_and_mul": override}))
-    assert layer.provider_name == ("custom_cuda" if override == "custom_cuda" else "hip")
+    assert layer.provider_name == "hip"
     x = torch.randn(5, 192, generator=torch.Generator().manual_seed(29)).bfloat16()
     out = layer(x.to(gpu))
     assert max_ulp_diff(out, silu_and_mul_fused(x)) <= 1

@@ -15,18 +15,16 @@ import torch
 
 from my_vllm_amd import ops
 from my_vllm_amd.attention_backend import (
-    AttentionBackend,
-    AttentionBackendRegistry,
-    AttentionPlan,
-    AttentionRoute,
     MI355XAttentionBackend,
     MI355XAttentionMetadata,
     MI355XSplitAttentionBackend,
+    integrate,
     make_decode_plan,
     make_decode_plan_listed,
     make_prefill_items,
 )
-from my_vllm_amd.context import BatchType, CommonAttentionMetadata
+from my_vllm_amd.contract import AttentionBackend, AttentionPlan, AttentionRoute, BatchType, CommonAttentionMetadata
+from tests import _foreign_contract as foreign
 
 KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
 
@@ -175,22 +173,88 @@ def test_support_reason_names_the_missing_capability():
                                            dtype=torch.bfloat16, device="cpu") is False
 
 
-def test_registry_contract():
-    names = AttentionBackendRegistry.names()
-    assert "mi355x" in names and "mi355x_split" in names
-    assert issubclass(AttentionBackendRegistry._BACKENDS["mi355x"], AttentionBackend)
+def test_backend_is_an_attention_backend_with_reference_capability_contract():
+    assert issubclass(MI355XAttentionBackend, AttentionBackend)
+    caps = dict(num_q_heads=16, num_kv_heads=4, head_dim=128, block_size=16, dtype=torch.bfloat16, device="cpu")
+    assert type(MI355XAttentionBackend.supports(**caps)) is bool
+    assert MI355XSplitAttentionBackend.default_attention_mode == "split"
+
+
+def _foreign_backends(registry_name: str):
+    class Registry(foreign.ForeignRegistry):
+        backends = {}
+
+    unified, split = integrate(Registry, foreign.ForeignBackendBase, foreign.ForeignPlan, foreign.ForeignRoute,
+                               foreign.ForeignBatchType, foreign.ForeignCommon,
+                               names=(registry_name, registry_name + "_split"))
+    return Registry, unified, split
+
+
+def test_integrate_registers_both_modes_in_a_foreign_registry():
+    registry, unified, split = _foreign_backends("mi355x")
+    assert registry.backends == {"mi355x": unified, "mi355x_split": split}
+    assert issubclass(unified, foreign.ForeignBackendBase) and issubclass(split, unified)
+    supported, reason = registry.support("mi355x", num_q_heads=16, num_kv_heads=4, head_dim=128, block_size=16,
+                                         dtype=torch.bfloat16, device="cpu")
+    assert supported is False and isinstance(reason, str) and reason  # no gfx950 in a CPU process
     with pytest.raises(ValueError):
-        AttentionBackendRegistry.register("auto", MI355XAttentionBackend)
-    with pytest.raises(ValueError):
-        AttentionBackendRegistry.register("", MI355XAttentionBackend)
-    with pytest.raises(ValueError):
-        AttentionBackendRegistry.register("mi355x", MI355XAttentionBackend)
+        integrate(registry, foreign.ForeignBackendBase, foreign.ForeignPlan, foreign.ForeignRoute,
+                  foreign.ForeignBatchType, foreign.ForeignCommon)  # names taken
+
+
+@pytest.mark.parametrize(
+    "q_lens,kv_lens,num_prefill,batch,unified_route,split_route",
+    [
+        ((1, 1), (21, 13), 0, "PURE_DECODE", "DECODE", "DECODE"),
+        ((5, 3), (21, 13), 2, "PURE_PREFILL", "PREFILL", "PREFILL"),
+        ((5, 1), (21, 13), 1, "MIXED", "MIXED_UNIFIED", "MIXED_SPLIT"),
+    ],
+)
+def test_foreign_family_plans_return_the_foreign_classes(q_lens, kv_lens, num_prefill, batch, unified_route,
+                                                         split_route):
+    _, unified, split = _foreign_backends("f")
+    common = foreign.to_foreign(_common(q_lens, kv_lens, num_prefill, trusted=True))
+    for cls, route in ((unified, unified_route), (split, split_route)):
+        host_cls = type("Host", (cls,), {"require_device_metadata": False})
+        plan = host_cls(16, 4, 128, 16, torch.bfloat16).build_plan(common)
+        assert type(plan) is foreign.ForeignPlan
+        assert plan.batch_type is foreign.ForeignBatchType[batch] and plan.route is foreign.ForeignRoute[route]
     with pytest.raises(TypeError):
-        AttentionBackendRegistry.register("not_a_backend", object)
-    with pytest.raises(RuntimeError):
-        # No gfx950 device in a CPU-only process: creation names the reason.
-        AttentionBackendRegistry.create("mi355x", num_q_heads=16, num_kv_heads=4, head_dim=128, block_size=16,
-                                        dtype=torch.bfloat16, device="cpu")
+        type("Host", (unified,), {"require_device_metadata": False})(16, 4, 128, 16, torch.bfloat16).build_plan(
+            _common(q_lens, kv_lens, num_prefill, trusted=True))  # this package's class is foreign to it
+
+
+def _record_launches(monkeypatch, backend):
+    calls = []
+    monkeypatch.setattr(type(backend), "_validate_inputs", lambda self, q, kc, vc: None)
+    for name in ("paged_decode", "paged_decode_store", "store_kvcache"):
+        monkeypatch.setattr(ops, name, lambda *a, _n=name, **k: calls.append(_n))
+    monkeypatch.setattr(type(backend), "_get_workspace", lambda self, nbytes, device: None)
+    return calls
+
+
+@pytest.mark.parametrize("family", ["own", "foreign"])
+@pytest.mark.parametrize("trusted", [True, False])
+def test_fused_store_path_is_taken_for_trusted_piece_list_decode(monkeypatch, family, trusted):
+    # forward_with_kv_store folds the store into the decode launch for the
+    # backend's own plan class and for a foreign family alike, and only for
+    # trusted (model-runner) metadata; otherwise the store runs first.
+    if family == "own":
+        cls = HostBackend
+        common = _common((1, 1, 1), (21, 13, 300), 0, trusted=trusted)
+    else:
+        _, unified, _ = _foreign_backends("g")
+        cls = type("Host", (unified,), {"require_device_metadata": False})
+        common = foreign.to_foreign(_common((1, 1, 1), (21, 13, 300), 0, trusted=trusted))
+    backend = cls(16, 4, 128, 16, torch.bfloat16)
+    plan = backend.build_plan(common)
+    assert plan.metadata.decode_wave_extra is not None  # piece lists
+    calls = _record_launches(monkeypatch, backend)
+    q = torch.zeros(3, 16, 128, dtype=torch.bfloat16)
+    kv = torch.zeros(3, 4, 128, dtype=torch.bfloat16)
+    cache = torch.zeros(40, 16, 4, 128, dtype=torch.bfloat16)
+    backend.forward_with_kv_store(q, kv, kv, cache, cache, common.slot_mapping, plan)
+    assert calls == (["paged_decode_store"] if trusted else ["store_kvcache", "paged_decode"])
 
 
 # ---------------------------------------------------------------------------

@@ -35,7 +35,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     lib = _native.load_library()
     for name in _declared_functions():
         assert hasattr(lib, name), f"{name} missing from {_native.LIB_PATH.name}"
-    assert lib.mva_abi_version() == 5 == _native.ABI_VERSION
+    assert lib.mva_abi_version() == _native.ABI_VERSION
 
 
 def test_library_binds_to_the_process_hip_runtime():
@@ -75,6 +75,15 @@ def test_dtype_codes_match_the_header():
     assert f"#define MVA_DTYPE_F16 {_native.DTYPE_CODES[torch.float16]}" in header
 
 
+def test_store_error_offset_matches_the_header_and_the_workspace_layout():
+    from my_vllm_amd import ops
+
+    header = (ROOT / "include" / "my_vllm_amd.h").read_text()
+    assert f"#define MVA_DECODE_STORE_ERROR_OFFSET {ops.DECODE_STORE_ERROR_OFFSET}" in header
+    # The word sits inside the scheduler area every decode workspace has.
+    assert ops.DECODE_STORE_ERROR_OFFSET + 4 <= _native.query("mva_decode_workspace_bytes", 0, 8, 1)
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_native, "_lib", None)
     monkeypatch.setattr(_native, "LIB_PATH", tmp_path / "absent.so")
@@ -91,3 +100,17 @@ def test_abi_revision_mismatch_raises(monkeypatch):
     monkeypatch.setattr(_native, "ABI_VERSION", _native.ABI_VERSION + 1)
     with pytest.raises(RuntimeError, match="ABI revision"):
         _native.load_library()
+
+
+def test_stale_library_without_a_new_entry_point_asks_for_a_rebuild(monkeypatch):
+    # A library built before an entry point was added must fail with the
+    # same "rebuild" RuntimeError (not an AttributeError), and
+    # native_available() must report False rather than raise.
+    monkeypatch.setattr(_native, "_lib", None)
+    monkeypatch.setattr(_native, "_load_error", _native._load_error)
+    signatures = dict(_native._SIGNATURES)
+    signatures["mva_entry_point_from_the_future"] = (ctypes.c_int, [])
+    monkeypatch.setattr(_native, "_SIGNATURES", signatures)
+    with pytest.raises(RuntimeError, match="rebuild"):
+        _native.load_library()
+    assert _native.native_available() is False

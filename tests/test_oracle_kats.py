@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 import torch
 
-from my_vllm_amd.context import BatchType, CommonAttentionMetadata
+from my_vllm_amd.contract import BatchType, CommonAttentionMetadata
 from oracle.reference import classify_batch, kv_store, page_csr, slot_mapping_for, split_page_csr
 
 KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())

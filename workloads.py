@@ -1,4 +1,5 @@
-"""Seeded synthetic batches for the hot path's benchmark configurations.
+"""Seeded synthetic batches for the hot path's benchmark configurations
+(used by the tests, the smoke check and bench.py; not part of the package).
 
 A batch is what the reference's ModelRunner would hand to the attention layer
 for one step (nanovllm/engine/model_runner.py:361-484): packed queries, new
@@ -19,7 +20,7 @@ from dataclasses import dataclass
 import numpy as np
 import torch
 
-from .context import CommonAttentionMetadata
+from my_vllm_amd.contract import CommonAttentionMetadata
 
 PAGE_SIZE = 16
 HEAD_DIM = 128
