@@ -23,9 +23,9 @@ from tests.test_gpu_prefill import expected, to_device
 pytestmark = pytest.mark.gpu
 
 
-def _both_ways(batch, device, dtype=torch.bfloat16, slots=None):
+def _both_ways(batch, device, dtype=torch.bfloat16, slots=None, trusted=True):
     hq, hkv = batch.q.shape[1], batch.k_cache.shape[2]
-    common, q, kc, vc = to_device(batch, device)
+    common, q, kc, vc = to_device(batch, device, trusted)
     k_new, v_new = batch.k_new.to(device), batch.v_new.to(device)
     slot_mapping = common.slot_mapping if slots is None else slots.to(device)
     backend = MI355XAttentionBackend(hq, hkv, 128, 16, dtype)
@@ -72,3 +72,69 @@ def test_claim_schedule_falls_back_to_the_separate_store(gpu, monkeypatch):
     assert torch.equal(sep, fused)
     stored = dataclasses.replace(batch, k_cache=kc_a.cpu(), v_cache=vc_a.cpu())
     assert_attention_close(fused, expected(stored))
+
+
+def _moved_slot_batch():
+    # Sequence 2's new row is sent to a slot in its first page instead of
+    # its last one: a page the decode launch may be streaming elsewhere.
+    batch = make_paged_batch(97, [1] * 5, [40, 7, 1000, 16, 129], 0, 16, 8)
+    slots = batch.common.slot_mapping.clone()
+    first_page = int(batch.common.block_tables[2, 0])
+    slots[2] = first_page * 16 + 3
+    return batch, slots
+
+
+def test_slot_outside_the_last_page_is_skipped_and_flagged(gpu):
+    batch, slots = _moved_slot_batch()
+    common, q, kc, vc = to_device(batch, gpu)
+    k_new, v_new = batch.k_new.to(gpu), batch.v_new.to(gpu)
+    backend = MI355XAttentionBackend(16, 8, 128, 16, torch.bfloat16)
+    plan = backend.build_plan(common)
+    assert common.trusted and plan.metadata.decode_wave_extra is not None
+    fused = backend.forward_with_kv_store(q, k_new, v_new, kc, vc, slots.to(gpu), plan).clone()
+    assert backend.fused_store_error() is True
+    assert backend.fused_store_error() is False  # cleared by the first read
+    # Expected: every other row stored, the moved one not at all.
+    kc_e, vc_e = batch.k_cache.to(gpu), batch.v_cache.to(gpu)
+    keep = torch.ones(5, dtype=torch.bool, device=gpu)
+    keep[2] = False
+    ops.store_kvcache(k_new[keep], v_new[keep], kc_e, vc_e, slots.to(gpu)[keep])
+    assert torch.equal(kc, kc_e) and torch.equal(vc, vc_e)
+    assert torch.equal(fused, backend.forward(q, k_new, v_new, kc_e, vc_e, plan))
+
+
+def test_untrusted_metadata_stores_first_like_the_reference(gpu):
+    batch, slots = _moved_slot_batch()
+    plan, sep, fused, (kc_a, vc_a), (kc_b, vc_b) = _both_ways(batch, gpu, slots=slots, trusted=False)
+    assert not plan.common.trusted and plan.metadata.decode_wave_extra is not None
+    assert torch.equal(kc_a, kc_b) and torch.equal(vc_a, vc_b)
+    assert torch.equal(sep, fused)
+
+
+def test_foreign_contract_family_takes_the_fused_path(gpu, monkeypatch):
+    # The backend built on another class family (as on the reference's own
+    # AttentionPlan) must still fold the store into the decode launch.
+    from my_vllm_amd.attention_backend import integrate
+    from tests import _foreign_contract as foreign
+
+    class Registry(foreign.ForeignRegistry):
+        backends = {}
+
+    unified, _ = integrate(Registry, foreign.ForeignBackendBase, foreign.ForeignPlan, foreign.ForeignRoute,
+                           foreign.ForeignBatchType, foreign.ForeignCommon)
+    batch = config_decode_small(seed=1)
+    common, q, kc, vc = to_device(batch, gpu)
+    k_new, v_new = batch.k_new.to(gpu), batch.v_new.to(gpu)
+    backend = unified(16, 8, 128, 16, torch.bfloat16)
+    plan = backend.build_plan(foreign.to_foreign(common))
+    assert type(plan) is foreign.ForeignPlan and plan.route is foreign.ForeignRoute.DECODE
+    fused_calls = []
+    real = ops.paged_decode_store
+    monkeypatch.setattr(ops, "paged_decode_store", lambda *a, **k: (fused_calls.append(1), real(*a, **k))[1])
+    kc_b, vc_b = kc.clone(), vc.clone()
+    fused = backend.forward_with_kv_store(q, k_new, v_new, kc_b, vc_b, common.slot_mapping, plan).clone()
+    assert fused_calls == [1]
+    own = MI355XAttentionBackend(16, 8, 128, 16, torch.bfloat16)
+    ops.store_kvcache(k_new, v_new, kc, vc, common.slot_mapping)
+    sep = own.forward(q, k_new, v_new, kc, vc, own.build_plan(common))
+    assert torch.equal(kc, kc_b) and torch.equal(vc, vc_b) and torch.equal(sep, fused)

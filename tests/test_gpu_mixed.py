@@ -75,3 +75,19 @@ def test_mixed_fp16(gpu, mode):
     out, _ = run_backend(batch, gpu, dtype=torch.float16, mode=mode)
     assert out.dtype == torch.float16
     assert_attention_close(out, expected(batch))
+
+
+@pytest.mark.parametrize("mode", ["unified", "split"])
+@pytest.mark.parametrize("case", range(3))
+def test_reference_numeric_cases(gpu, mode, case):
+    # The reference's paged pure/MIXED numeric cases
+    # (tests/test_attention_backend.py:367-418): Hq=16, Hkv=4, seeds 307+i,
+    # both attention modes; case 2 is its MIXED batch ((5, 1), (21, 13), 1).
+    q_lens, kv_lens, num_prefill = [((5, 3), (21, 13), 2), ((1, 1), (21, 13), 0), ((5, 1), (21, 13), 1)][case]
+    batch = make_paged_batch(307 + case, list(q_lens), list(kv_lens), num_prefill, 16, 4)
+    out, plan = run_backend(batch, gpu, mode=mode)
+    route = {0: AttentionRoute.PREFILL, 1: AttentionRoute.DECODE,
+             2: AttentionRoute.MIXED_UNIFIED if mode == "unified" else AttentionRoute.MIXED_SPLIT}[case]
+    assert plan.route is route
+    assert out.shape == batch.q.shape and out.dtype == torch.bfloat16
+    assert_attention_close(out, expected(batch))
