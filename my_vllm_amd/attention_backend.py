@@ -135,8 +135,10 @@ def make_decode_plan(
     pieces each (clamped to ``[min_piece_pages, max_piece_pages]``); short
     pieces let the wavefronts on faster CUs take more of the work.  A piece
     is ``(seq, page_begin, page_end, chunk, n_chunks, part_base, q_row,
-    kv_head)``; a segment cut into ``n_chunks > 1`` pieces owns that many
-    split-K partial slots from ``part_base``.  Pieces are ordered longest
+    kv_head)``; a sequence cut into ``n_chunks > 1`` pieces per KV head owns
+    that many split-K partial slots from ``part_base``, shared by its KV
+    heads (the kernel's slot is ``(part_base + chunk) * Hkv + kv_head``, as
+    with piece lists).  Pieces are ordered longest
     first, then sequence-major with the KV head fastest (the head slices of
     one page are neighbours in the cache).  Returns ``(items, waves,
     num_part_slots)`` with ``waves = min(num_waves, len(items))``, the grid to
@@ -163,21 +165,23 @@ def make_decode_plan(
     # Near-equal cut of L pages into n pieces: piece k covers [k*L//n, (k+1)*L//n).
     begin = (chunk * len_of) // n_of
     end = ((chunk + 1) * len_of) // n_of
-    split_sizes = np.where(nchunks > 1, nchunks, 0)
-    part_base = np.cumsum(split_sizes) - split_sizes
+    # Every KV head of a sequence has the same length and so the same cut:
+    # partial slots are numbered per sequence.
+    seq_split = np.where(nchunks[::num_kv_heads] > 1, nchunks[::num_kv_heads], 0)
+    seq_base = np.cumsum(seq_split) - seq_split
     items = np.zeros((seg_of.size, ops.DECODE_ITEM_INTS), dtype=np.int32)
     items[:, 0] = first_seq + seg_of // num_kv_heads
     items[:, 1] = begin
     items[:, 2] = end
     items[:, 3] = chunk
     items[:, 4] = n_of
-    items[:, 5] = part_base[seg_of]
+    items[:, 5] = seq_base[seg_of // num_kv_heads]
     items[:, 6] = first_q_row + seg_of // num_kv_heads
     items[:, 7] = seg_of % num_kv_heads
     order = np.argsort(-(end - begin), kind="stable")
     items = items[order]
     waves = max(1, min(int(num_waves), items.shape[0]))
-    return items, waves, int(split_sizes.sum())
+    return items, waves, int(seq_split.sum())
 
 
 # Workgroups of a piece-list decode launch fill 8 wave slots per CU (the

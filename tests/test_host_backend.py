@@ -281,9 +281,12 @@ def _check_decode_plan(counts, hkv, waves, per_wave, min_pages):
         assert sorted(p[2] for p in pieces) == list(range(nc))
         if nc > 1:
             base = pieces[0][4]
-            assert all(p[4] == base for p in pieces)
-            assert not used & set(range(base, base + nc)) and base + nc <= slots
-            used |= set(range(base, base + nc))
+            assert all(p[4] == base for p in pieces) and base + nc <= slots
+            # The kernel's partial slot of chunk c: (base + c) * Hkv + h.
+            ids = {(base + c) * hkv + h for c in range(nc)}
+            assert not used & ids
+            used |= ids
+    assert len(used) <= slots * hkv
     lengths = items[:, 2] - items[:, 1]
     assert np.all(np.diff(lengths) <= 0), "pieces are listed longest first"
     return items, nw, slots
