@@ -248,6 +248,37 @@ int mva_paged_decode_graph(const void* q, int64_t q_token_stride, int64_t q_head
                            int64_t workspace_bytes, int num_q_heads, int num_kv_heads, int head_dim,
                            int page_size, float softmax_scale, int dtype, void* stream);
 
+/* Bytes of the static device scratch mva_paged_decode_noalloc uses per GPU. */
+#define MVA_DECODE_STATIC_SCRATCH_BYTES (64LL << 20)
+
+/*
+ * mva_paged_decode for callers that cannot allocate device memory: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * No counterpart in the reference (its FlashInfer wrappers own workspaces the
+ * caller allocated).  The decode workspace lives in a static device array of
+ * MVA_DECODE_STATIC_SCRATCH_BYTES that each GPU holds until the process ends;
+ * the call allocates and frees nothing.  Arguments as mva_paged_decode,
+ * without workspace / workspace_bytes.
+ *   - Plans whose workspace (mva_decode_workspace_bytes(num_part_slots,
+ *     num_kv_heads, num_q_heads / num_kv_heads)) exceeds the scratch are
+ *     rejected with an error before anything is launched.
+ *   - The first call on a device looks up that device's scratch address and
+ *     clears its scheduler counters with one small kernel on `stream`; make it
+ *     outside graph capture.  The kernels leave the counters cleared again.
+ *   - Every call on one GPU shares that GPU's scratch: calls that overlap on
+ *     one GPU (other streams, other threads) race.  Calls in stream order,
+ *     one after another, are safe.
+ */
+int mva_paged_decode_noalloc(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                             const void* k_cache, const void* v_cache, int64_t num_pages,
+                             int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
+                             int64_t block_table_stride, const int32_t* seq_lens, const int32_t* items,
+                             int64_t num_items, int64_t num_waves, const int32_t* wave_extra,
+                             int waves_per_group, const int32_t* merges, int64_t num_merges,
+                             int64_t num_part_slots, void* out, int64_t out_token_stride,
+                             int64_t out_head_stride, int num_q_heads, int num_kv_heads, int head_dim,
+                             int page_size, float softmax_scale, int dtype, void* stream);
+
 /* Query-token rows per prefill workgroup tile for a GQA ratio (128 / ratio),
  * or -1 for invalid head counts. */
 int mva_prefill_tile_tokens(int num_q_heads, int num_kv_heads);

@@ -101,6 +101,19 @@ _SIGNATURES = {
             _i32, _i32, _i32, _i32, _f32, _i32, _c_void_p,
         ],
     ),
+    "mva_paged_decode_noalloc": (
+        _i32,
+        [
+            _c_void_p, _i64, _i64,  # q, q_token_stride, q_head_stride
+            _c_void_p, _c_void_p, _i64, _i64, _i64,  # k_cache, v_cache, num_pages, page_stride, token_stride
+            _c_void_p, _i64, _c_void_p,  # block_tables, block_table_stride, seq_lens
+            _c_void_p, _i64, _i64,  # items, num_items, num_waves
+            _c_void_p, _i32,  # wave_extra, waves_per_group
+            _c_void_p, _i64, _i64,  # merges, num_merges, num_part_slots
+            _c_void_p, _i64, _i64,  # out, out_token_stride, out_head_stride
+            _i32, _i32, _i32, _i32, _f32, _i32, _c_void_p,  # heads, head_dim, page, scale, dtype, stream
+        ],
+    ),
     "mva_prefill_tile_tokens": (_i32, [_i32, _i32]),
     "mva_paged_prefill": (
         _i32,
@@ -130,7 +143,7 @@ _SIGNATURES = {
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 # The C ABI revision these signatures describe (mva_abi_version()).
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

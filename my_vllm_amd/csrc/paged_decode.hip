@@ -3,6 +3,8 @@
 #include "mva_capi.h"
 #include "paged_decode.h"
 
+#include <mutex>
+
 namespace mva {
 namespace {
 
@@ -256,4 +258,83 @@ extern "C" int mva_paged_decode_graph(const void* q, int64_t q_token_stride, int
   else return set_error("paged attention: dtype must be bf16 or fp16");
   if (rc) return rc;
   return launch_decode_merge(p, merges, merge_capacity, dtype, s);
+}
+
+// ---- decode with no allocation: static device scratch ---------------------
+//
+// mva_paged_decode_noalloc runs mva_paged_decode's kernels with the decode
+// workspace (scheduler counters + split-K partials) placed in `scratch`, a
+// file-scope device array, so a call allocates nothing.  Each GPU holds its
+// own copy for the life of the process.  In host code `scratch` names a
+// host-side stand-in: its device address on the current GPU comes from
+// hipGetSymbolAddress, looked up once per device and kept in
+// g_scratch_addr; only that address is ever handed to a kernel.
+
+namespace mva {
+namespace {
+
+constexpr int64_t kStaticScratchBytes = int64_t(64) << 20;  // MVA_DECODE_STATIC_SCRATCH_BYTES
+constexpr int kMaxScratchDevices = 64;
+
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+std::mutex g_scratch_mutex;
+void* g_scratch_addr[kMaxScratchDevices] = {};
+
+// Zeroes `words` 32-bit words with vector stores (graph-capturable, unlike
+// a memset node).
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int words) {
+  for (int i = threadIdx.x; i < words; i += 256) p[i] = 0u;
+}
+
+// The current device's scratch address.  The first call on a device looks it
+// up and clears the scheduler area with one kernel on `stream`; the decode
+// kernels leave it cleared again on exit, so later calls clear nothing.
+int static_scratch(hipStream_t stream, void** addr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+    return set_error("paged attention (no-alloc): no usable current HIP device");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr)
+      return set_error("paged attention (no-alloc): hipGetSymbolAddress of the static scratch failed");
+    hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(256), 0, stream, (uint32_t*)ptr, kDecodeSchedBytes / 4);
+    if (const int rc = check_launch("paged attention (no-alloc) scratch clear")) return rc;
+    g_scratch_addr[dev] = ptr;
+  }
+  *addr = g_scratch_addr[dev];
+  return 0;
+}
+
+}  // namespace
+}  // namespace mva
+
+extern "C" int mva_paged_decode_noalloc(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                                        const void* k_cache, const void* v_cache, int64_t num_pages,
+                                        int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
+                                        int64_t block_table_stride, const int32_t* seq_lens,
+                                        const int32_t* items, int64_t num_items, int64_t num_waves,
+                                        const int32_t* wave_extra, int waves_per_group,
+                                        const int32_t* merges, int64_t num_merges,
+                                        int64_t num_part_slots, void* out, int64_t out_token_stride,
+                                        int64_t out_head_stride, int num_q_heads, int num_kv_heads,
+                                        int head_dim, int page_size, float softmax_scale, int dtype,
+                                        void* stream) {
+  using namespace mva;
+  if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads || num_part_slots < 0)
+    return set_error("paged attention (no-alloc): invalid head counts or partial slot count");
+  const int64_t need = decode_workspace_bytes(num_part_slots, num_kv_heads, num_q_heads / num_kv_heads);
+  if (need > kStaticScratchBytes)
+    return set_error("paged attention (no-alloc): the plan's split-K partials exceed the 64 MiB static "
+                     "scratch; use mva_paged_decode with a workspace");
+  hipStream_t s = (hipStream_t)stream;
+  void* ws = nullptr;
+  if (const int rc = static_scratch(s, &ws)) return rc;
+  return mva_paged_decode(q, q_token_stride, q_head_stride, k_cache, v_cache, num_pages, page_stride,
+                          token_stride, block_tables, block_table_stride, seq_lens, items, num_items, num_waves,
+                          wave_extra, waves_per_group, merges, num_merges, num_part_slots, out,
+                          out_token_stride, out_head_stride, ws, kStaticScratchBytes, num_q_heads,
+                          num_kv_heads, head_dim, page_size, softmax_scale, dtype, stream);
 }
