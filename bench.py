@@ -15,8 +15,12 @@ timed with HIP events on the stream it is launched on; ``cpu_baseline`` times
 the CPU oracle (the reference's fp32 paged-attention restatement) on a
 bounded sample of the same workload on the host cores.
 
+Every figure is the median of 5 timed regions (HIP events on the launch
+stream).  Prefill and MIXED inputs are the CPU-seeded draws the parity tests
+check; the 10.7 GB long-decode batch is drawn on the GPU, as its test does.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra]
-       python bench.py --only {decode,long_decode,prefill,mixed,silu,copy} [--steps K]
+       python bench.py --only {decode,decode_store,long_decode,prefill,mixed,silu,store,copy} [--steps K]
 The ``--only`` forms run one workload's kernel K times and print one line;
 they are the programs the committed rocprofv3 summaries profile (``copy`` is
 a 256 MiB device copy used to calibrate the byte counters).
@@ -27,12 +31,15 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
 import torch
 
 HBM_PEAK_GBPS = 8000.0
+# Timed regions per figure; the median is reported.
+REPEATS = 5
 BF16_PEAK_TFLOPS = 2500.0
 METRIC = "paged GQA decode HBM GB/s (% of peak); mixed-batch attention tokens/s"
 
@@ -44,7 +51,8 @@ def parse_args(argv=None):
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-extra", action="store_true", help="headline and roofline only")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
-    ap.add_argument("--only", choices=["decode", "long_decode", "prefill", "mixed", "silu", "copy"],
+    ap.add_argument("--only", choices=["decode", "decode_store", "long_decode", "prefill", "mixed", "silu", "store",
+                                       "copy"],
                     help="run one workload's kernel --steps times (for profilers) and exit")
     return ap.parse_args(argv)
 
@@ -59,19 +67,27 @@ def to_device(batch, device):
     return common
 
 
-def time_launches(fn, iters: int, warmup: int) -> float:
-    """Average ms per call of `fn`, timed with HIP events on the current stream."""
+def time_launches(fn, iters: int, warmup: int, repeats: int = 1) -> float:
+    """ms per call of `fn`: the median over `repeats` timed regions of `iters`
+    calls each, timed with HIP events on the current stream (the stream the
+    kernels are launched on).  `fn(i)` gets a running call index, which the
+    callers use to rotate input copies."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(iters):
-        fn(i)
-    end.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / iters
+    per_call = []
+    n = warmup
+    for _ in range(repeats):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(iters):
+            fn(n)
+            n += 1
+        end.record()
+        torch.cuda.synchronize()
+        per_call.append(start.elapsed_time(end) / iters)
+    return statistics.median(per_call)
 
 
 def decode_bytes(batch, num_q_heads, num_kv_heads, elem=2) -> int:
@@ -118,7 +134,7 @@ def headline(args, device):
         backend.forward_with_kv_store(q, k_new, v_new, kc, vc, common.slot_mapping, plan, store)
 
     torch.cuda.synchronize()
-    ms_step = time_launches(step, args.steps, args.warmup)
+    ms_step = time_launches(step, args.steps, args.warmup, repeats=REPEATS)
     step_bytes = decode_bytes(batch, hq, hkv) + store_bytes(len(batch.kv_lengths), hkv)
 
     # Roofline of the decode kernel alone: direct launches (no store), same
@@ -135,7 +151,7 @@ def headline(args, device):
                          md.num_decode_part_slots, out, ws, backend.softmax_scale,
                          md.decode_wave_extra, md.decode_waves_per_group)
 
-    ms_decode = time_launches(decode_only, max(args.steps, 200), args.warmup)
+    ms_decode = time_launches(decode_only, max(args.steps, 500), args.warmup, repeats=REPEATS)
     dec_bytes = decode_bytes(batch, hq, hkv)
     achieved = dec_bytes / ms_decode / 1e6
     return {
@@ -161,11 +177,40 @@ def headline(args, device):
     }
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_rate(fn, nbytes: int, seconds: float) -> tuple[float, int]:
+    """GB/s of `fn` (moving `nbytes` per call) over about `seconds` of calls."""
+    fn()  # warm up
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    return nbytes / dt / 1e9, reps
+
+
 def cpu_baseline(batch, seconds: float):
-    """The CPU oracle (fp32 paged attention, the reference's test restatement)
-    on the first 16 sequences of the headline batch, as K/V GB/s."""
+    """The reference's native paths as restated by the CPU oracle, timed on
+    this host's cores: fp32 paged attention (the reference's test oracle; its
+    only CPU attention) on the first 16 sequences of the headline batch
+    (`value`, GB/s of K/V), plus the SiLU-and-mul eager path at the
+    Qwen3-0.6B MLP shape and the index_copy_ KV store of 16384 tokens."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from oracle.reference import paged_attention
+    from oracle.reference import kv_store_index_copy, paged_attention, silu_and_mul_eager
+    from workloads import silu_input
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
@@ -173,23 +218,37 @@ def cpu_baseline(batch, seconds: float):
     q_rows = sum(batch.query_lengths[:n])
     args = (batch.q[:q_rows], batch.k_cache, batch.v_cache, batch.common.block_tables[:n],
             batch.query_lengths[:n], batch.kv_lengths[:n])
-    paged_attention(*args)  # warm up
-    reps = 0
-    t0 = time.perf_counter()
-    while True:
-        paged_attention(*args)
-        reps += 1
-        if time.perf_counter() - t0 >= seconds:
-            break
-    dt = (time.perf_counter() - t0) / reps
     kv_bytes = sum(batch.kv_lengths[:n]) * 8 * 128 * 2 * 2
+    attn_gbps, attn_reps = _cpu_rate(lambda: paged_attention(*args), kv_bytes, seconds)
+
+    x = silu_input(4096, 6144, seed=0)
+    silu_gbps, silu_reps = _cpu_rate(lambda: silu_and_mul_eager(x), 75497472, seconds / 2)
+
+    tokens, hkv = 16384, 8
+    gen = torch.Generator().manual_seed(5)
+    key = torch.randn(tokens, hkv, 128, generator=gen).bfloat16()
+    value = torch.randn(tokens, hkv, 128, generator=gen).bfloat16()
+    pages = tokens // 16 + 64
+    k_cache = torch.zeros(pages, 16, hkv, 128, dtype=torch.bfloat16)
+    v_cache = torch.zeros_like(k_cache)
+    slots = torch.randperm(pages * 16, generator=gen)[:tokens].to(torch.int32)
+    store_gbps, store_reps = _cpu_rate(lambda: kv_store_index_copy(key, value, k_cache, v_cache, slots),
+                                       store_bytes(tokens, hkv), seconds / 2)
     return {
-        "value": round(kv_bytes / dt / 1e9, 3),
+        "value": round(attn_gbps, 3),
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"oracle.reference.paged_attention (fp32 einsum) on sequences 0-15 of the headline "
-                  f"batch ({sum(batch.kv_lengths[:n])} keys), {reps} reps in {seconds:.0f}s",
+        "cpu_model": cpu_model(),
+        "sample": f"oracle.reference.paged_attention (fp32 einsum, the reference's test oracle) on sequences "
+                  f"0-15 of the headline batch ({sum(batch.kv_lengths[:n])} keys), {attn_reps} reps in "
+                  f"{seconds:.0f}s on {cores} threads",
+        "legs": {
+            "silu_and_mul_eager_4096x6144_GBps": round(silu_gbps, 3),
+            "silu_and_mul_eager_reps": silu_reps,
+            "kv_store_index_copy_16384tok_GBps": round(store_gbps, 3),
+            "kv_store_index_copy_reps": store_reps,
+        },
     }
 
 
@@ -246,7 +305,8 @@ def extra_measurements(device, steps: int):
     del ga, gb
 
     # PURE_PREFILL with prefix, Qwen3-8B.
-    batch = config_prefill(seed=2, device=device, rng_device="cuda")
+    # The same CPU-seeded draw the parity tests check.
+    batch = config_prefill(seed=2, device=device)
     ms = attn_case(batch, 32, 8)
     flops = 4 * 128 * 32 * causal_pairs(batch.query_lengths, batch.kv_lengths)
     res["prefill_TFLOPs"] = round(flops / ms / 1e9, 1)
@@ -254,7 +314,7 @@ def extra_measurements(device, steps: int):
     del batch
 
     # MIXED, Qwen3-8B, token budget 8192.
-    batch = config_mixed(seed=3, device=device, rng_device="cuda")
+    batch = config_mixed(seed=3, device=device)
     t = sum(batch.query_lengths)
     ms_u = attn_case(batch, 32, 8, "unified")
     ms_s = attn_case(batch, 32, 8, "split")
@@ -395,11 +455,51 @@ def run_only(args, device):
                           "launches": n}))
         return 0
     if args.only == "silu":
+        # 8 rotated inputs (600 MB, past the 256 MB Infinity Cache).
         x = silu_input(4096, 6144, seed=0).to(device)
-        for _ in range(n):
-            ops.silu_and_mul(x)
+        xs = [x.clone() for _ in range(8)]
+        for i in range(n):
+            ops.silu_and_mul(xs[i % 8])
         torch.cuda.synchronize()
-        print(json.dumps({"only": "silu", "bytes_per_launch": 75497472, "launches": n}))
+        print(json.dumps({"only": "silu", "bytes_per_launch": 75497472, "launches": n, "rotated_inputs": 8}))
+        return 0
+    if args.only == "store":
+        # 16384 new tokens (a 16K-token prefill chunk) at 8 KV heads, scattered
+        # to random slots of a 1.1 GB cache pair; 4 rotated inputs.
+        tokens, hkv = 16384, 8
+        gen = torch.Generator(device=device).manual_seed(5)
+        keys = [torch.randn(tokens, hkv, 128, generator=gen, device=device).bfloat16() for _ in range(4)]
+        vals = [torch.randn(tokens, hkv, 128, generator=gen, device=device).bfloat16() for _ in range(4)]
+        pages = 32768
+        k_cache = torch.zeros(pages, 16, hkv, 128, dtype=torch.bfloat16, device=device)
+        v_cache = torch.zeros_like(k_cache)
+        slots = [torch.randperm(pages * 16, generator=gen, device=device)[:tokens].to(torch.int32)
+                 for _ in range(4)]
+        for i in range(n):
+            ops.store_kvcache(keys[i % 4], vals[i % 4], k_cache, v_cache, slots[i % 4])
+        torch.cuda.synchronize()
+        print(json.dumps({"only": "store", "bytes_per_launch": store_bytes(tokens, hkv), "launches": n,
+                          "rotated_inputs": 4}))
+        return 0
+    if args.only == "decode_store":
+        # The headline step's kernel: the KV store folded into the decode launch.
+        from my_vllm_amd.layers import KVCacheStore
+        from my_vllm_amd.custom_op import CustomOpConfig
+
+        batch, hq, hkv = config_decode_small(seed=1), 16, 8
+        common = to_device(batch, device)
+        q = batch.q.to(device)
+        k_new, v_new = batch.k_new.to(device), batch.v_new.to(device)
+        caches = [(batch.k_cache.to(device), batch.v_cache.to(device)) for _ in range(4)]
+        backend = MI355XAttentionBackend(hq, hkv, 128, 16, torch.bfloat16)
+        store = KVCacheStore(CustomOpConfig(platform="cuda"))
+        plan = backend.build_plan(common)
+        for i in range(n):
+            kc, vc = caches[i % 4]
+            backend.forward_with_kv_store(q, k_new, v_new, kc, vc, common.slot_mapping, plan, store)
+        torch.cuda.synchronize()
+        print(json.dumps({"only": "decode_store", "bytes_per_launch": decode_bytes(batch, hq, hkv)
+                          + store_bytes(len(batch.kv_lengths), hkv), "launches": n}))
         return 0
     if args.only in ("decode", "long_decode"):
         if args.only == "decode":
@@ -425,7 +525,7 @@ def run_only(args, device):
                           "waves": md.num_decode_waves, "pieces": md.num_decode_items}))
         return 0
     batch = (config_prefill if args.only == "prefill" else config_mixed)(seed=2 if args.only == "prefill" else 3,
-                                                                        device=device, rng_device="cuda")
+                                                                        device=device)
     backend = MI355XAttentionBackend(32, 8, 128, 16, torch.bfloat16)
     common = to_device(batch, device)
     q = batch.q.to(device)
@@ -482,6 +582,8 @@ def main(argv=None):
             "decode_pieces": head["items"],
             "decode_schedule": head["schedule"],
         },
+        "timing": f"median of {REPEATS} timed regions of {args.steps} steps each (HIP events), "
+                  "4 KV-cache copies rotated",
         "roofline": head["roofline"],
         "cpu_baseline": cpu,
         "extra": extra,

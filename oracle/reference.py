@@ -130,6 +130,21 @@ def kv_store(
     flat_v[slots] = value[valid]
 
 
+def kv_store_index_copy(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                        slot_mapping: torch.Tensor) -> None:
+    """The same scatter in torch, as the reference's CPU path runs it:
+    ``index_copy_`` of the rows whose slot is ``>= 0`` into the caches viewed
+    as ``[-1, H, D]`` (nanovllm/layers/attention.py:69-85).  Timed as the
+    store's CPU baseline; pinned to ``kv_store`` by the tests."""
+    if slot_mapping.numel() != key.shape[0]:
+        raise ValueError("slot_mapping must contain one slot per token")
+    h, d = key.shape[-2:]
+    keep = slot_mapping >= 0
+    rows = slot_mapping[keep].long()
+    k_cache.view(-1, h, d).index_copy_(0, rows, key[keep])
+    v_cache.view(-1, h, d).index_copy_(0, rows, value[keep])
+
+
 # ---------------------------------------------------------------------------
 # Paged / ragged attention
 # ---------------------------------------------------------------------------

@@ -159,3 +159,22 @@ def test_golden_fixture_is_current():
     module = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(module)
     assert module.KATS == KATS
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_torch_index_copy_store_equals_the_numpy_store(seed):
+    # The torch form timed as the store's CPU baseline writes the same bits.
+    from oracle.reference import kv_store_index_copy
+
+    rng = np.random.default_rng(seed)
+    n, h, d, pages = 37, 2, 8, 5
+    key = rng.integers(-2**15, 2**15, size=(n, h, d), dtype=np.int16)
+    value = rng.integers(-2**15, 2**15, size=(n, h, d), dtype=np.int16)
+    slots = rng.permutation(pages * 16)[:n].astype(np.int32)
+    slots[rng.random(n) < 0.2] = -1
+    kc = rng.integers(-2**15, 2**15, size=(pages, 16, h, d), dtype=np.int16)
+    vc = kc.copy()
+    kt, vt = torch.from_numpy(kc.copy()), torch.from_numpy(vc.copy())
+    kv_store(key, value, kc, vc, slots)
+    kv_store_index_copy(torch.from_numpy(key), torch.from_numpy(value), kt, vt, torch.from_numpy(slots))
+    assert np.array_equal(kt.numpy(), kc) and np.array_equal(vt.numpy(), vc)
