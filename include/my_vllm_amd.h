@@ -283,16 +283,25 @@ int mva_paged_decode_noalloc(const void* q, int64_t q_token_stride, int64_t q_he
  * or -1 for invalid head counts. */
 int mva_prefill_tile_tokens(int num_q_heads, int num_kv_heads);
 
+/* Bytes of the prefill workspace (the device-built tile list) for at most
+ * max_tiles query tiles, or -1 for an invalid count. */
+int64_t mva_prefill_workspace_bytes(int64_t max_tiles);
+
 /*
  * Ragged causal chunked prefill over prefix-cached pages (same cache and q/out
- * conventions as mva_paged_decode).  Sequence s has query rows
+ * conventions as mva_paged_decode).  Sequence s < num_seqs has query rows
  * query_start_loc[s] .. query_start_loc[s+1] - 1 (q_s rows) and seq_lens[s]
  * keys including them; query i sees keys j <= seq_lens[s] - q_s + i.  The new
  * tokens' K/V are read from the cache (store them first).
- *   items [num_items, 4] int32 query tiles {seq, first_token, 0, 0}; a tile
- *         covers mva_prefill_tile_tokens() tokens x all query heads of one KV
- *         head; tiles past a sequence's query count exit without writing.
- * Launch grid = num_items x num_kv_heads workgroups of 256 threads.
+ * The work list is built on the device from query_start_loc and seq_lens
+ * (nothing is read back to the host): one query tile per
+ * mva_prefill_tile_tokens() tokens x all query heads of a KV head, longest
+ * context first, written into `workspace` (mva_prefill_workspace_bytes(
+ * max_tiles) bytes, 16-byte aligned).  max_tiles must bound the tile count,
+ * e.g. num_prefill_tokens / tile_tokens + num_seqs; tiles beyond it are not
+ * run.  A sequence with no queries, or more queries than keys, is skipped.
+ * A persistent grid of workgroups then streams the tiles.  Launches that
+ * share a workspace must not overlap.
  * Replaces FlashInfer BatchPrefillWithPagedKVCacheWrapper.plan/run on the
  * reference's PREFILL route (nanovllm/layers/attention_backend.py:810-825,
  * :992-994) and the prefill half of MIXED_SPLIT (:858-873, :1015-1019).
@@ -301,15 +310,18 @@ int mva_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_stri
                       const void* k_cache, const void* v_cache, int64_t num_pages,
                       int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
                       int64_t block_table_stride, const int32_t* seq_lens,
-                      const int32_t* query_start_loc, const int32_t* items, int64_t num_items,
-                      void* out, int64_t out_token_stride, int64_t out_head_stride,
-                      int num_q_heads, int num_kv_heads, int head_dim, int page_size,
-                      float softmax_scale, int dtype, void* stream);
+                      const int32_t* query_start_loc, int64_t num_seqs, int64_t max_tiles,
+                      void* workspace, int64_t workspace_bytes, void* out, int64_t out_token_stride,
+                      int64_t out_head_stride, int num_q_heads, int num_kv_heads, int head_dim,
+                      int page_size, float softmax_scale, int dtype, void* stream);
 
 /*
- * MIXED batch in one launch: prefill tiles (as mva_paged_prefill) write the
- * rows of the leading prefill sequences and decode pieces (as
- * mva_paged_decode) write the trailing decode rows of the same `out` buffer.
+ * MIXED batch in one launch: prefill tiles write the rows of the leading
+ * prefill sequences and decode pieces (as mva_paged_decode) write the
+ * trailing decode rows of the same `out` buffer.
+ *   prefill_items [num_prefill_items, 4] int32 query tiles {seq, first_token,
+ *         0, 0} (mva_prefill_tile_tokens() tokens each); tiles past a
+ *         sequence's query count exit without writing.
  * Replaces FlashInfer BatchAttention.plan/run on the reference's MIXED_UNIFIED
  * route (nanovllm/layers/attention_backend.py:841-857, :998-1009).
  */

@@ -115,13 +115,14 @@ _SIGNATURES = {
         ],
     ),
     "mva_prefill_tile_tokens": (_i32, [_i32, _i32]),
+    "mva_prefill_workspace_bytes": (_i64, [_i64]),
     "mva_paged_prefill": (
         _i32,
         [
             _c_void_p, _i64, _i64,  # q, q_token_stride, q_head_stride
             _c_void_p, _c_void_p, _i64, _i64, _i64,  # k_cache, v_cache, num_pages, page_stride, token_stride
             _c_void_p, _i64, _c_void_p, _c_void_p,  # block_tables, stride, seq_lens, query_start_loc
-            _c_void_p, _i64,  # items, num_items
+            _i64, _i64, _c_void_p, _i64,  # num_seqs, max_tiles, workspace, workspace_bytes
             _c_void_p, _i64, _i64,  # out, out_token_stride, out_head_stride
             _i32, _i32, _i32, _i32, _f32, _i32, _c_void_p,
         ],
@@ -143,7 +144,7 @@ _SIGNATURES = {
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 # The C ABI revision these signatures describe (mva_abi_version()).
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -66,8 +66,9 @@ class MI355XAttentionMetadata:
     runs its own piece list (``make_decode_plan_listed``); without it the
     wavefronts claim pieces (``make_decode_plan``).  ``decode_merges`` lists the split segments
     (``ops.decode_merge_list``) whose partials the merge kernel combines.
-    ``prefill_items`` is int32 ``[num_prefill_items, 4]`` query tiles (see
-    ``make_prefill_items``).  ``kv_indptr`` is the page CSR offset list (host
+    ``prefill_items`` is int32 ``[num_prefill_items, 4]`` query tiles of the
+    single MIXED launch (see ``make_prefill_items``); the PREFILL and split
+    routes plan their tiles on the device, within ``prefill_max_tiles``.  ``kv_indptr`` is the page CSR offset list (host
     ints): sequence ``s`` owns pages ``block_tables[s, :kv_indptr[s+1]-kv_indptr[s]]``.
     """
 
@@ -89,6 +90,8 @@ class MI355XAttentionMetadata:
     decode_host_plan: tuple | None = None
     prefill_items: torch.Tensor | None = None
     num_prefill_items: int = 0
+    # Bound on the prefill query tiles (sizes the device-built tile list).
+    prefill_max_tiles: int = 0
 
     @property
     def is_cacheless(self) -> bool:
@@ -468,6 +471,7 @@ class MI355XAttentionBackendMixin:
         self._route_counts = {route.value: 0 for route in self.route_type}
         self._output_buffer: torch.Tensor | None = None
         self._workspace: torch.Tensor | None = None
+        self._prefill_workspace: torch.Tensor | None = None
         self._active_graph_state: MI355XFullDecodeGraphState | None = None
         # (key, value, slot_mapping) of the step while forward_with_kv_store
         # folds the KV store into the decode launch.
@@ -610,7 +614,13 @@ class MI355XAttentionBackendMixin:
                 decode_host_plan = (items, wave_extra, merges, groups)
         prefill_items = None
         num_prefill_items = 0
+        prefill_max_tiles = 0
         if common.num_prefill_seqs:
+            prefill_max_tiles = ops.prefill_max_tiles(common.num_prefill_tokens, common.num_prefill_seqs,
+                                                      self.num_q_heads, self.num_kv_heads)
+        if common.num_prefill_seqs and common.num_decode_seqs and self.attention_mode == "unified":
+            # The single MIXED launch takes host-built tiles; PREFILL and the
+            # split route plan their tiles on the device.
             num_prefill = common.num_prefill_seqs
             kv_ub = counts[:num_prefill] * self.block_size
             if common.trusted:
@@ -646,6 +656,7 @@ class MI355XAttentionBackendMixin:
             decode_host_plan=decode_host_plan,
             prefill_items=prefill_items,
             num_prefill_items=num_prefill_items,
+            prefill_max_tiles=prefill_max_tiles,
         )
 
     def build_plan(self, common, metadata: MI355XAttentionMetadata | None = None):
@@ -686,6 +697,14 @@ class MI355XAttentionBackendMixin:
             buffer = torch.empty_like(q)
             self._output_buffer = buffer
         return buffer[:required]
+
+    def _get_prefill_workspace(self, max_tiles: int, device: torch.device) -> torch.Tensor:
+        nbytes = ops.prefill_workspace_bytes(max_tiles)
+        ws = self._prefill_workspace
+        if ws is None or ws.numel() < nbytes or ws.device != device:
+            ws = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+            self._prefill_workspace = ws
+        return ws
 
     def _get_workspace(self, nbytes: int, device: torch.device) -> torch.Tensor | None:
         if nbytes <= 0:
@@ -1006,20 +1025,18 @@ class MI355XAttentionBackendMixin:
         table = np.full((q_lens.size, int(counts.max())), -1, dtype=np.int64)
         for s_idx, (base, c) in enumerate(zip(first_page, counts)):
             table[s_idx, :c] = np.arange(base, base + c)
-        tile = ops.PREFILL_ROWS // (self.num_q_heads // self.num_kv_heads)
-        items = make_prefill_items(q_lens, q_lens, tile)
-        host = np.concatenate([slots, table.reshape(-1), q_lens, items.reshape(-1)]).astype(np.int32)
+        host = np.concatenate([slots, table.reshape(-1), q_lens]).astype(np.int32)
         flat = _to_device(host, device)
         n_slot, n_table = slots.size, table.size
         slot_mapping = flat[:n_slot]
         block_tables = flat[n_slot:n_slot + n_table].view(table.shape)
-        seq_lens = flat[n_slot + n_table:n_slot + n_table + q_lens.size]
-        prefill_items = flat[n_slot + n_table + q_lens.size:].view(items.shape)
+        seq_lens = flat[n_slot + n_table:]
         pool = torch.empty((2, int(counts.sum()), PAGE_SIZE, self.num_kv_heads, self.head_dim), dtype=self.dtype,
                            device=device)
         ops.store_kvcache(k, v, pool[0], pool[1], slot_mapping)
-        ops.paged_prefill(q, pool[0], pool[1], block_tables, seq_lens, common.query_start_loc, prefill_items,
-                          items.shape[0], output, self.softmax_scale)
+        max_tiles = ops.prefill_max_tiles(q.size(0), q_lens.size, self.num_q_heads, self.num_kv_heads)
+        ops.paged_prefill(q, pool[0], pool[1], block_tables, seq_lens, common.query_start_loc, q_lens.size,
+                          max_tiles, self._get_prefill_workspace(max_tiles, device), output, self.softmax_scale)
 
     def _run_prefill(self, q, k_cache, v_cache, common, metadata: MI355XAttentionMetadata, output) -> None:
         ops.paged_prefill(
@@ -1029,8 +1046,9 @@ class MI355XAttentionBackendMixin:
             metadata.block_tables,
             metadata.seq_lens,
             metadata.query_start_loc,
-            metadata.prefill_items,
-            metadata.num_prefill_items,
+            common.num_prefill_seqs,
+            metadata.prefill_max_tiles,
+            self._get_prefill_workspace(metadata.prefill_max_tiles, q.device),
             output,
             self.softmax_scale,
         )

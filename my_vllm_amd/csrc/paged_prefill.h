@@ -90,14 +90,20 @@ __device__ inline float pair_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// One prefill work item.  k0/k1 and v0/v1 must be four distinct __shared__
-// arrays of kPrefillTileBytes: with distinct objects the compiler can tell
-// that a DMA into one buffer does not alias reads of another and does not
-// wait for in-flight DMAs before every LDS read.
+// One query tile of one prefill sequence, as the kernel needs it.  pg0 /
+// pg1 are the calling wave's pages of 64-key tiles 0 and 1 (wave w reads page
+// w of the 4 in a tile).
+struct PrefillWork {
+  int s, t0, q0, q_len, kv, ntiles, full_tiles, npages, pg0, pg1;
+};
+
+// Runs one prefill work item.  k0/k1 and v0/v1 must be four distinct
+// __shared__ arrays of kPrefillTileBytes (distinct objects keep the compiler
+// from treating reads of one buffer as dependent on DMAs into another).
 template <typename T>
-__device__ __attribute__((always_inline)) inline void prefill_item(
-    const PrefillParams& p, const int32_t* __restrict__ it, int h, lds_u8* k0, lds_u8* k1, lds_u8* v0,
-    lds_u8* v1) {
+__device__ __attribute__((always_inline)) inline void prefill_core(const PrefillParams& p, const PrefillWork& wk,
+                                                                   int h, lds_u8* k0, lds_u8* k1, lds_u8* v0,
+                                                                   lds_u8* v1) {
   typedef typename Elem<T>::v8 V8;
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -105,12 +111,11 @@ __device__ __attribute__((always_inline)) inline void prefill_item(
   const int ln = lane & 31;
   const int hi = lane >> 5;
 
-  const int s = it[0];
-  const int t0 = it[1];
-  const int q0 = p.query_start_loc[s];
-  const int q_len = p.query_start_loc[s + 1] - q0;
-  if (t0 >= q_len) return;  // tile past this sequence's queries (host sizes conservatively)
-  const int kv = p.seq_lens[s];
+  const int s = wk.s;
+  const int t0 = wk.t0;
+  const int q0 = wk.q0;
+  const int q_len = wk.q_len;
+  const int kv = wk.kv;
   const int G = p.group;
   const int BMT = p.tile_tokens;
   const int base_pos = kv - q_len;  // absolute position of query token 0
@@ -122,10 +127,8 @@ __device__ __attribute__((always_inline)) inline void prefill_item(
   const bool row_ok = g < G && tq < q_len;
   const int pos = row_ok ? base_pos + tq : -1;  // keys j <= pos are visible
 
-  const int t_end = min(t0 + BMT, q_len);
-  const int kv_end = base_pos + t_end;  // keys [0, kv_end) are needed by some row
-  const int ntiles = (kv_end + kPrefillKeys - 1) / kPrefillKeys;
-  const int full_tiles = min((base_pos + t0 + 1) / kPrefillKeys, ntiles);  // tiles no row masks
+  const int ntiles = wk.ntiles;
+  const int full_tiles = wk.full_tiles;  // tiles no row masks
 
   // Q fragments (B operand of S^T = K Q^T): k-step kk covers d-chunk 2*kk + hi.
   V8 qf[8];
@@ -140,7 +143,7 @@ __device__ __attribute__((always_inline)) inline void prefill_item(
   const T* kc = (const T*)p.k_cache + h * kHeadDim;
   const T* vc = (const T*)p.v_cache + h * kHeadDim;
   const int32_t* bt = p.block_tables + (int64_t)s * p.bt_stride;
-  const int npages = (kv_end + kPageSize - 1) / kPageSize;
+  const int npages = wk.npages;
 
   // Page id of this wave's page (page w of the 4 in a tile) of `tile`; pages
   // past the needed range clamp to the last needed page (masked later).
@@ -182,15 +185,18 @@ __device__ __attribute__((always_inline)) inline void prefill_item(
   // Softmax of S(t): P fragments for the PV k-steps and the O rescale factor.
   auto softmax = [&](int tile, f32x16 (&st)[2], V8 (&pf)[4], float& alpha, auto masked_tag) {
     constexpr bool masked = decltype(masked_tag)::value;
-    const int j0 = tile * kPrefillKeys;
+    // Element i of block mt holds key tile*64 + 32*mt + 8*(i/4) + 4*hi + i%4;
+    // it is visible when that key is <= pos, i.e. when the compile-time part
+    // 32*mt + 8*(i/4) + i%4 is <= lim.  (Comparing against one per-lane limit
+    // keeps 32 per-lane key offsets from being hoisted out of the loop.)
+    const int lim = pos - tile * kPrefillKeys - 4 * hi;
     float tmax = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         if constexpr (masked) {
-          const int key = j0 + 32 * mt + 8 * (i >> 2) + 4 * hi + (i & 3);
-          if (key > pos) st[mt][i] = -INFINITY;
+          if (32 * mt + 8 * (i >> 2) + (i & 3) > lim) st[mt][i] = -INFINITY;
         }
         tmax = fmaxf(tmax, st[mt][i]);
       }
@@ -245,14 +251,14 @@ __device__ __attribute__((always_inline)) inline void prefill_item(
   };
 
   // Prologue: K(0), K(1), V(0) in flight, then S(0).
-  int pg_v = page_of(1);   // page of V(t+1) at iteration t (= page of K(t+1))
-  int pg_k = page_of(2);   // page of K(t+2) at iteration t
+  int pg_v = __builtin_amdgcn_readfirstlane(wk.pg1);  // page of V(t+1) at iteration t (= page of K(t+1))
   {
-    const int pg0 = page_of(0);
+    const int pg0 = __builtin_amdgcn_readfirstlane(wk.pg0);
     dma_k(pg0, k0);
     if (ntiles > 1) dma_k(pg_v, k1);
     dma_v(pg0, v0);
   }
+  int pg_k = page_of(2);  // page of K(t+2) at iteration t
   __builtin_amdgcn_s_waitcnt(kVmcnt0);
   __syncthreads();
   f32x16 st_a[2], st_b[2];  // S(t) lives in st_a for even t, st_b for odd t
@@ -317,6 +323,81 @@ __device__ __attribute__((always_inline)) inline void prefill_item(
       for (int e = 0; e < 4; ++e) wv[e] = (T)(o[dt][4 * bk + e] * inv);
       *reinterpret_cast<typename Elem<T>::v4*>(op + 32 * dt + 8 * bk + 4 * hi) = wv;
     }
+}
+
+
+// ---- exact, device-built tile list and the persistent prefill launch -------
+//
+// Plan buffer (int32): a header (tile count and per-head claim counters),
+// then the tiles from word kPrefillPlanHeaderInts, kPrefillPlanItemInts words
+// each:
+//   {seq, t0, q0, q_len, kv, ntiles, full_tiles, npages,
+//    page ids of 64-key tile 0 (4 pages), of tile 1 (4 pages)}
+// for the BMT-token query tile [t0, t0 + BMT) of prefill sequence `seq`
+// (query rows q0 .. q0 + q_len - 1, kv keys), which needs `ntiles` 64-key
+// tiles (`npages` pages), the first `full_tiles` of them below every row's
+// causal bound.  Page ids past npages repeat the last page; ids outside the
+// cache read as page 0.
+constexpr int kPrefillPlanItemInts = 16;
+// Header: word 0 = tile count; the claim counter of KV head h at word
+// kPrefillPlanLineInts * (1 + h), each on its own 128-byte line.
+constexpr int kPrefillPlanLineInts = 32;
+constexpr int kPrefillPlanMaxHeads = 127;
+constexpr int kPrefillPlanHeaderInts = kPrefillPlanLineInts * (1 + kPrefillPlanMaxHeads);
+// Sequences the planner sorts longest-context first (more are planned in
+// batch order).
+constexpr int kPrefillPlanSortMax = 2048;
+
+// A work item of the host-built list {seq, t0, 0, 0}: its query count, keys
+// and first pages are read here (tiles past the sequence's queries exit).
+template <typename T>
+__device__ __attribute__((always_inline)) inline void prefill_item(
+    const PrefillParams& p, const int32_t* __restrict__ it, int h, lds_u8* k0, lds_u8* k1, lds_u8* v0,
+    lds_u8* v1) {
+  PrefillWork wk;
+  wk.s = it[0];
+  wk.t0 = it[1];
+  wk.q0 = p.query_start_loc[wk.s];
+  wk.q_len = p.query_start_loc[wk.s + 1] - wk.q0;
+  if (wk.t0 >= wk.q_len) return;  // tile past this sequence's queries (host sizes conservatively)
+  wk.kv = p.seq_lens[wk.s];
+  const int base_pos = wk.kv - wk.q_len;
+  const int kv_end = base_pos + min(wk.t0 + p.tile_tokens, wk.q_len);  // keys [0, kv_end) are needed
+  wk.ntiles = (kv_end + kPrefillKeys - 1) / kPrefillKeys;
+  wk.full_tiles = min((base_pos + wk.t0 + 1) / kPrefillKeys, wk.ntiles);
+  wk.npages = (kv_end + kPageSize - 1) / kPageSize;
+  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int32_t* bt = p.block_tables + (int64_t)wk.s * p.bt_stride;
+  auto page = [&](int i) {
+    const int pg = sload(bt, min(i, wk.npages - 1));
+    return (pg >= 0 && pg < p.num_pages) ? pg : 0;
+  };
+  wk.pg0 = page(w);
+  wk.pg1 = page(kPrefillKeys / kPageSize + w);
+  prefill_core<T>(p, wk, h, k0, k1, v0, v1);
+}
+
+// The tile list mva_paged_prefill builds on the device: the record of tile
+// i at word kPrefillPlanHeaderInts + i * kPrefillPlanItemInts (see
+// kPrefillPlanHeaderInts), read with one scalar load.
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(4))) const i32x16 const_i32x16;
+
+__device__ inline PrefillWork plan_work(const int32_t* plan, int idx) {
+  const i32x16 d = ((const_i32x16*)(plan + kPrefillPlanHeaderInts))[idx];
+  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  PrefillWork wk;
+  wk.s = d[0];
+  wk.t0 = d[1];
+  wk.q0 = d[2];
+  wk.q_len = d[3];
+  wk.kv = d[4];
+  wk.ntiles = d[5];
+  wk.full_tiles = d[6];
+  wk.npages = d[7];
+  wk.pg0 = w == 0 ? d[8] : w == 1 ? d[9] : w == 2 ? d[10] : d[11];
+  wk.pg1 = w == 0 ? d[12] : w == 1 ? d[13] : w == 2 ? d[14] : d[15];
+  return wk;
 }
 
 }  // namespace mva

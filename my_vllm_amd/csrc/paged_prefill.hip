@@ -19,17 +19,160 @@ int launch_decode_merge(const DecodeParams& p, const int32_t* merges, int64_t nu
 
 namespace {
 
+// Exact tile list of a prefill batch, built on the device from
+// query_start_loc / seq_lens (one workgroup; see kPrefillPlanHeaderInts for
+// the format).  Sequences are ordered longest context first (up to
+// kPrefillPlanSortMax sequences; batch order beyond), and a sequence's tiles
+// largest key count first, so the tiles that read one sequence's pages run
+// together and long work starts early.  A sequence with no queries, or with
+// more queries than keys, gets no tile.  At most `capacity` tiles are
+// written; word 0 receives their number.
+__global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* __restrict__ qsl,
+                                                            const int32_t* __restrict__ seq_lens,
+                                                            const int32_t* __restrict__ block_tables,
+                                                            int64_t bt_stride, int64_t num_pages, int num_seqs,
+                                                            int tile_tokens, int num_kv_heads,
+                                                            int32_t* __restrict__ plan, int capacity) {
+  // Sequences in plan order (rank -> sequence) and the first tile of each
+  // rank; sequences beyond kPrefillPlanSortMax keep batch order and are
+  // planned in later rounds of the same steps.
+  __shared__ int kv_of[kPrefillPlanSortMax];
+  __shared__ int order[kPrefillPlanSortMax];
+  __shared__ int first_tile[kPrefillPlanSortMax + 1];
+  __shared__ int scan[1024];
+  __shared__ int carry;
+  const int tid = threadIdx.x;
+  const bool sorted = num_seqs <= kPrefillPlanSortMax;
+  if (tid == 0) carry = 0;
+  if (sorted) {
+    for (int s = tid; s < num_seqs; s += 1024) kv_of[s] = seq_lens[s];
+    __syncthreads();
+    for (int s = tid; s < num_seqs; s += 1024) {
+      const int mine = kv_of[s];
+      int rank = 0;
+      for (int o = 0; o < num_seqs; ++o) {
+        const int v = kv_of[o];
+        rank += (v > mine) || (v == mine && o < s);
+      }
+      order[rank] = s;
+    }
+  }
+  __syncthreads();
+  int32_t* out = plan + kPrefillPlanHeaderInts;
+  for (int c = 0; c < num_seqs; c += kPrefillPlanSortMax) {
+    const int span = min(kPrefillPlanSortMax, num_seqs - c);
+    // Tiles per rank in this round, then their exclusive prefix sum.
+    for (int r0 = 0; r0 < span; r0 += 1024) {
+      const int r = r0 + tid;
+      int nt = 0;
+      if (r < span) {
+        const int s = sorted ? order[r] : c + r;
+        const int q_len = qsl[s + 1] - qsl[s];
+        const int kv = seq_lens[s];
+        if (q_len > 0 && kv >= q_len) nt = (q_len + tile_tokens - 1) / tile_tokens;
+      }
+      scan[tid] = nt;
+      __syncthreads();
+      for (int off = 1; off < 1024; off <<= 1) {
+        const int add = tid >= off ? scan[tid - off] : 0;
+        __syncthreads();
+        scan[tid] += add;
+        __syncthreads();
+      }
+      if (r < span) first_tile[r] = carry + scan[tid] - nt;
+      __syncthreads();
+      if (tid == 0) carry += scan[1023];
+      __syncthreads();
+    }
+    if (tid == 0) first_tile[span] = carry;
+    __syncthreads();
+    // One tile per thread: find its rank by binary search, write its record.
+    const int lo_tile = first_tile[0], hi_tile = first_tile[span];
+    for (int i = lo_tile + tid; i < hi_tile && i < capacity; i += 1024) {
+      int lo = 0, hi = span - 1;  // last rank whose first tile is <= i
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (first_tile[mid] <= i) lo = mid;
+        else hi = mid - 1;
+      }
+      const int s = sorted ? order[lo] : c + lo;
+      const int q0 = qsl[s];
+      const int q_len = qsl[s + 1] - q0;
+      const int kv = seq_lens[s];
+      const int nt = (q_len + tile_tokens - 1) / tile_tokens;
+      const int jt = i - first_tile[lo];
+      const int t0 = (nt - 1 - jt) * tile_tokens;  // largest key count first
+      const int bpos = kv - q_len;
+      const int kv_end = bpos + min(t0 + tile_tokens, q_len);
+      const int ntiles = (kv_end + kPrefillKeys - 1) / kPrefillKeys;
+      const int full = min((bpos + t0 + 1) / kPrefillKeys, ntiles);
+      const int npages = (kv_end + kPageSize - 1) / kPageSize;
+      const int32_t* bt = block_tables + (int64_t)s * bt_stride;
+      int pg[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int v = bt[min(k, npages - 1)];
+        pg[k] = (v >= 0 && v < num_pages) ? v : 0;
+      }
+      int32_t* d = out + (int64_t)i * kPrefillPlanItemInts;
+      *reinterpret_cast<int4*>(d) = int4{s, t0, q0, q_len};
+      *reinterpret_cast<int4*>(d + 4) = int4{kv, ntiles, full, npages};
+      *reinterpret_cast<int4*>(d + 8) = int4{pg[0], pg[1], pg[2], pg[3]};
+      *reinterpret_cast<int4*>(d + 12) = int4{pg[4], pg[5], pg[6], pg[7]};
+    }
+    __syncthreads();
+  }
+  if (tid == 0) plan[0] = min(carry, capacity);
+  if (tid < num_kv_heads) plan[kPrefillPlanLineInts * (1 + tid)] = 0;  // claim counters
+}
+
+// Persistent prefill: workgroup b serves KV head b % num_kv_heads (so head
+// h stays on XCD h when the head count divides 8).  The workgroups of a head
+// take tiles of the plan in order from that head's claim counter, one claim
+// ahead: the next tile is claimed when a tile starts and is known by the
+// time it ends, so the grid never waits on dispatch and faster CUs simply
+// run more tiles.
 template <typename T>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void paged_prefill_kernel(
-    PrefillParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void paged_prefill_stream_kernel(
+    PrefillParams p, int32_t* __restrict__ plan) {
   __shared__ __attribute__((aligned(16))) uint8_t k0[kPrefillTileBytes];
   __shared__ __attribute__((aligned(16))) uint8_t k1[kPrefillTileBytes];
   __shared__ __attribute__((aligned(16))) uint8_t v0[kPrefillTileBytes];
   __shared__ __attribute__((aligned(16))) uint8_t v1[kPrefillTileBytes];
+  __shared__ int claimed;
   const int h = (int)(blockIdx.x % (uint32_t)p.num_kv_heads);
-  const int item = (int)(blockIdx.x / (uint32_t)p.num_kv_heads);
-  prefill_item<T>(p, p.items + (int64_t)item * kPrefillItemInts, h, (lds_u8*)k0, (lds_u8*)k1, (lds_u8*)v0,
-                  (lds_u8*)v1);
+  const int n = sload(plan, 0);
+  int* const ctr = plan + kPrefillPlanLineInts * (1 + h);
+  auto claim = [&]() { return __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  if (threadIdx.x == 0) claimed = claim();
+  __syncthreads();
+  int idx = claimed;
+  while (idx < n) {
+    const PrefillWork wk = plan_work(plan, idx);
+    int next = 0;
+    if (threadIdx.x == 0) next = claim();
+    prefill_core<T>(p, wk, h, (lds_u8*)k0, (lds_u8*)k1, (lds_u8*)v0, (lds_u8*)v1);
+    __syncthreads();  // every wave is done with this tile's LDS before `claimed` changes
+    if (threadIdx.x == 0) claimed = next;
+    __syncthreads();
+    idx = claimed;
+  }
+}
+
+// Resident workgroups of the persistent prefill per CU (the kernel's
+// registers allow two 256-thread workgroups per CU).
+constexpr int kPrefillStreamGroupsPerCu = 2;
+
+int device_cu_count() {
+  static int counts[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (counts[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    counts[dev] = cus;
+  }
+  return counts[dev];
 }
 
 // Workgroup roles of the MIXED launch: the decode workgroups come first, in
@@ -134,27 +277,51 @@ extern "C" int mva_prefill_tile_tokens(int num_q_heads, int num_kv_heads) {
   return mva::kPrefillRows / (num_q_heads / num_kv_heads);
 }
 
+extern "C" int64_t mva_prefill_workspace_bytes(int64_t max_tiles) {
+  if (max_tiles < 0 || max_tiles > 0x7fffffffLL / mva::kPrefillPlanItemInts) return -1;
+  return (mva::kPrefillPlanHeaderInts + max_tiles * mva::kPrefillPlanItemInts) * 4;
+}
+
 extern "C" int mva_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_stride,
                                  const void* k_cache, const void* v_cache, int64_t num_pages,
                                  int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
                                  int64_t block_table_stride, const int32_t* seq_lens,
-                                 const int32_t* query_start_loc, const int32_t* items, int64_t num_items,
-                                 void* out, int64_t out_token_stride, int64_t out_head_stride,
-                                 int num_q_heads, int num_kv_heads, int head_dim, int page_size,
-                                 float softmax_scale, int dtype, void* stream) {
+                                 const int32_t* query_start_loc, int64_t num_seqs, int64_t max_tiles,
+                                 void* workspace, int64_t workspace_bytes, void* out, int64_t out_token_stride,
+                                 int64_t out_head_stride, int num_q_heads, int num_kv_heads, int head_dim,
+                                 int page_size, float softmax_scale, int dtype, void* stream) {
   using namespace mva;
   PrefillParams p;
   int rc = fill_prefill_params(p, q, q_token_stride, q_head_stride, k_cache, v_cache, num_pages, page_stride,
                                token_stride, block_tables, block_table_stride, seq_lens, query_start_loc,
-                               items, num_items, out, out_token_stride, out_head_stride, num_q_heads,
+                               nullptr, 0, out, out_token_stride, out_head_stride, num_q_heads,
                                num_kv_heads, head_dim, page_size, softmax_scale);
   if (rc) return rc;
-  if (num_items == 0) return 0;
-  const dim3 grid((uint32_t)(num_items * num_kv_heads));
+  if (dtype != kBF16 && dtype != kF16) return set_error("paged attention: dtype must be bf16 or fp16");
+  if (num_seqs < 0 || num_seqs > 0x7fffffffLL) return set_error("paged attention: invalid sequence count");
+  const int64_t need = mva_prefill_workspace_bytes(max_tiles);
+  if (need < 0) return set_error("paged attention: invalid tile capacity");
+  if (num_seqs == 0 || max_tiles == 0) return 0;
+  if (workspace == nullptr || workspace_bytes < need)
+    return set_error("paged attention: prefill workspace too small for max_tiles");
+  if (((uintptr_t)workspace) % 16) return set_error("paged attention: prefill workspace must be 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == kBF16) hipLaunchKernelGGL(paged_prefill_kernel<__bf16>, grid, dim3(256), 0, s, p);
-  else if (dtype == kF16) hipLaunchKernelGGL(paged_prefill_kernel<_Float16>, grid, dim3(256), 0, s, p);
-  else return set_error("paged attention: dtype must be bf16 or fp16");
+  int32_t* plan = (int32_t*)workspace;
+  if (num_kv_heads > kPrefillPlanMaxHeads) return set_error("paged attention: at most 127 KV heads");
+  hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(1024), 0, s, query_start_loc, seq_lens, block_tables,
+                     block_table_stride, num_pages, (int)num_seqs, p.tile_tokens, num_kv_heads, plan,
+                     (int)max_tiles);
+  rc = check_launch("paged_prefill plan");
+  if (rc) return rc;
+  // Persistent grid: enough workgroups to fill every CU, a whole number per
+  // KV head, never more than the tiles can use.
+  int64_t per_head = (int64_t)kPrefillStreamGroupsPerCu * device_cu_count() / num_kv_heads;
+  per_head = per_head < 1 ? 1 : (per_head > max_tiles ? max_tiles : per_head);
+  const dim3 grid((uint32_t)(per_head * num_kv_heads));
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(paged_prefill_stream_kernel<__bf16>, grid, dim3(256), 0, s, p, plan);
+  else
+    hipLaunchKernelGGL(paged_prefill_stream_kernel<_Float16>, grid, dim3(256), 0, s, p, plan);
   return check_launch("paged_prefill");
 }
 

@@ -19,8 +19,12 @@ DECODE_ITEM_INTS = 8
 MAX_CHUNK_PAGES = 128
 # Query rows per prefill workgroup (kPrefillRows): G heads x 128 // G tokens.
 PREFILL_ROWS = 128
-# int32 fields per prefill work item (kPrefillItemInts).
+# int32 fields per prefill work item of the MIXED launch (kPrefillItemInts).
 PREFILL_ITEM_INTS = 4
+# Device-built prefill tile list: header ints (tile count + per-head claim
+# counters) and ints per tile record (kPrefillPlanHeaderInts / ItemInts).
+PREFILL_PLAN_HEADER_INTS = 32 * 128
+PREFILL_PLAN_ITEM_INTS = 16
 
 
 def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
@@ -529,6 +533,20 @@ def _tail_args(q, k_cache, softmax_scale):
     )
 
 
+def prefill_max_tiles(num_prefill_tokens: int, num_prefill_seqs: int, num_q_heads: int, num_kv_heads: int) -> int:
+    """Bound on the query tiles of a prefill batch: sum(ceil(q_s / tile)) <=
+    tokens // tile + sequences."""
+    tile = PREFILL_ROWS // (num_q_heads // num_kv_heads)
+    return num_prefill_tokens // tile + num_prefill_seqs
+
+
+def prefill_workspace_bytes(max_tiles: int) -> int:
+    nbytes = int(_native.query("mva_prefill_workspace_bytes", max_tiles))
+    if nbytes < 0:
+        raise ValueError("invalid prefill tile capacity")
+    return nbytes
+
+
 def paged_prefill(
     q: torch.Tensor,
     k_cache: torch.Tensor,
@@ -536,21 +554,24 @@ def paged_prefill(
     block_tables: torch.Tensor,
     seq_lens: torch.Tensor,
     query_start_loc: torch.Tensor,
-    items: torch.Tensor,
-    num_items: int,
+    num_seqs: int,
+    max_tiles: int,
+    workspace: torch.Tensor,
     out: torch.Tensor,
     softmax_scale: float,
 ) -> None:
-    """Launch the ragged causal prefill kernel over prepared query tiles.
+    """Launch the ragged causal prefill over the first ``num_seqs`` sequences.
 
-    ``items`` int32 ``[n, 4]`` = (sequence, first query token of the tile, 0, 0);
-    tiles past a sequence's query count exit without writing.
+    The query tiles are planned on the device from ``query_start_loc`` and
+    ``seq_lens`` into ``workspace`` (at least
+    ``prefill_workspace_bytes(max_tiles)`` bytes); ``max_tiles`` must bound
+    the tile count (see :func:`prefill_max_tiles`).
     """
     _native.call(
         "mva_paged_prefill",
         *_paged_args(q, k_cache, v_cache, block_tables, seq_lens),
-        query_start_loc.data_ptr(),
-        items.data_ptr(), num_items,
+        query_start_loc.data_ptr(), int(num_seqs), int(max_tiles),
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(),
         out.data_ptr(), out.stride(0), out.stride(1),
         *_tail_args(q, k_cache, softmax_scale),
     )

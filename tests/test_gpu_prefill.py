@@ -10,6 +10,7 @@ stale rows, fp16, trusted vs untrusted metadata, and the cacheless warmup.
 import pytest
 import torch
 
+from my_vllm_amd import ops
 from my_vllm_amd.attention_backend import MI355XAttentionBackend
 from my_vllm_amd.contract import AttentionRoute
 from my_vllm_amd.contract import BatchType
@@ -175,3 +176,56 @@ def test_cacheless_warmup_runs_the_prefill_kernel(gpu, lengths, hq, hkv):
     out = backend.forward(q.to(gpu), kvd[:, :hkv], kvd[:, hkv:], empty, empty, plan)
     assert out.data_ptr() == backend._get_reusable_attention_output(q.to(gpu)).data_ptr()
     assert_attention_close(out, ragged_attention(q, k.contiguous(), v.contiguous(), lengths))
+
+
+def _expected_tiles(q_lens, kv_lens, tile):
+    """The tile list the device planner must write: sequences by context
+    length (longest first, ties by index), each sequence's tiles by key count
+    (largest first), as {seq, t0, q0, q_len, kv, ntiles, full, npages} and
+    the page-table slots of the first two 64-key tiles' 8 pages (clamped to
+    the last needed page)."""
+    starts = [0]
+    for n in q_lens:
+        starts.append(starts[-1] + n)
+    rows = []
+    for s in sorted(range(len(q_lens)), key=lambda i: (-kv_lens[i], i)):
+        q, kv = q_lens[s], kv_lens[s]
+        if q <= 0 or kv < q:
+            continue
+        nt = -(-q // tile)
+        for j in range(nt):
+            t0 = (nt - 1 - j) * tile
+            kv_end = kv - q + min(t0 + tile, q)
+            ntiles = -(-kv_end // 64)
+            npages = -(-kv_end // 16)
+            rows.append([s, t0, starts[s], q, kv, ntiles, min((kv - q + t0 + 1) // 64, ntiles), npages]
+                        + [min(i, npages - 1) for i in range(8)])
+    return rows
+
+
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (16, 1), (12, 4)])
+def test_device_tile_plan_is_exact(gpu, hq, hkv):
+    # Exact tiles from the device's query offsets: no tile past a sequence's
+    # queries, ordered as the host restatement orders them.
+    q = [1, 37, 130, 64, 700, 3, 700]
+    kv = [1, 37 + 16 * 9, 130, 64 + 80, 2000, 3, 700]
+    batch = make_paged_batch(131, q, kv, len(q), hq, hkv)
+    out, plan = run_backend(batch, gpu)
+    assert_attention_close(out, expected(batch))
+    # run_backend drops the backend; plan again on a kept one to read its workspace.
+    backend = MI355XAttentionBackend(hq, hkv, 128, 16, torch.bfloat16)
+    common, qd, kc, vc = to_device(batch, gpu)
+    p = backend.build_plan(common)
+    empty = qd.new_empty((0, hkv, 128))
+    backend.forward(qd, empty, empty, kc, vc, p)
+    torch.cuda.synchronize()
+    backend_ws = backend._prefill_workspace.view(torch.int32).cpu()
+    tile = 128 // (hq // hkv)
+    want = _expected_tiles(q, kv, tile)
+    assert int(backend_ws[0]) == len(want) <= p.metadata.prefill_max_tiles
+    head, rec = ops.PREFILL_PLAN_HEADER_INTS, ops.PREFILL_PLAN_ITEM_INTS
+    got = backend_ws[head:head + rec * len(want)].view(-1, rec).tolist()
+    # Page slots -> the sequence's page ids.
+    bt = batch.common.block_tables
+    want = [r[:8] + [int(bt[r[0], i]) for i in r[8:]] for r in want]
+    assert got == want
