@@ -90,6 +90,22 @@ __device__ inline float pair_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Two probabilities rounded to the storage type and packed into one word.
+template <typename T>
+struct PackedPair;
+template <>
+struct PackedPair<__bf16> {
+  typedef __bf16 x2 __attribute__((ext_vector_type(2)));
+  __device__ static inline uint32_t pack(float a, float b) { return __builtin_bit_cast(uint32_t, x2{(__bf16)a, (__bf16)b}); }
+};
+template <>
+struct PackedPair<_Float16> {
+  typedef _Float16 x2 __attribute__((ext_vector_type(2)));
+  __device__ static inline uint32_t pack(float a, float b) {
+    return __builtin_bit_cast(uint32_t, x2{(_Float16)a, (_Float16)b});
+  }
+};
+
 // One query tile of one prefill sequence, as the kernel needs it.  pg0 /
 // pg1 are the calling wave's pages of 64-key tiles 0 and 1 (wave w reads page
 // w of the 4 in a tile).
@@ -164,79 +180,105 @@ __device__ __attribute__((always_inline)) inline void prefill_core(const Prefill
     dma16_x4_saddr(vc + (int64_t)page * p.page_stride, voff, (uint32_t)(uintptr_t)(buf + 4096 * w));
   };
 
-  // S^T of one tile: st[mt][i] = S[query ln][key 32*mt + 8*(i/4) + 4*hi + i%4].
-  auto qk = [&](const lds_u8* kb, f32x16 (&st)[2]) {
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      st[mt] = f32x16{};
-      const int key = 32 * mt + ln;
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk)
-        st[mt] = Elem<T>::mfma32(lds_ld16<V8>(kb + klds_off(key, 2 * kk + hi)), qf[kk], st[mt]);
-    }
+  // The pipeline is written in issue order as steps of one MFMA each, its
+  // LDS operand read one step ahead, a few vector instructions of the
+  // softmax beside it, and a scheduling barrier after it.  The matrix cores
+  // and the vector ALU of a SIMD overlap only a few vector instructions per
+  // MFMA; spreading the softmax evenly over the MFMAs of both phases keeps
+  // it in the MFMA shadow instead of in a block of its own.
+  //
+  // Element i of S block mt: st[mt][i] = S[query ln][key 32*mt + 8*(i/4) +
+  // 4*hi + i%4] (the C layout of S^T = K Q^T).  Its probability goes to PV
+  // k-step kk = 2*mt + (i/4)/2, word ((i/4) % 2)*2 + (i%4)/2 of pw[kk] (two
+  // packed values per word: the B layout of P^T).
+  auto kread = [&](const lds_u8* kb, int j) {  // QK step j: chain j % 2, k-step j / 2
+    return lds_ld16<V8>(kb + klds_off(32 * (j & 1) + ln, 2 * (j >> 1) + hi));
+  };
+  // PV step j: k-step j / 4, d-tile j % 4.  16-lane group a = lane/16 covers
+  // d offset 16*(a&1) of the 32-d tile and keys 4*hi.. of each 8-key block;
+  // supplier lane ti gives row 4*hi + ti/4 at d offset 4*(ti%4).
+  const int ti = lane & 15;
+  const int dgrp = (lane >> 4) & 1;
+  const int vlane_off = (4 * hi + (ti >> 2)) * 64 + (2 * dgrp + ((ti >> 1) & 1)) * 16 + (ti & 1) * 8;
+  auto vread = [&](const lds_u8* vb, int j) {
+    const lds_u8* a = vb + vlane_off + (j >> 2) * 4096 + (j & 3) * 1024;
+    return __builtin_bit_cast(V8, __builtin_shufflevector(lds_ld_tr16(a), lds_ld_tr16(a + 512), 0, 1, 2, 3, 4, 5, 6,
+                                                          7));
   };
 
   f32x16 o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{};
-  float m = -INFINITY;
-  float l = 0.f;
+  float m = -INFINITY;  // reference max (log2 units) of the tiles so far
+  float l = 0.f;        // row sum of P, relative to m
+  float m_use = 0.f;    // m, or 0 while no key is visible
+  float alpha = 1.0f;   // O rescale factor of the tile whose P is computed next
+  float tmax = -INFINITY;
 
-  // Softmax of S(t): P fragments for the PV k-steps and the O rescale factor.
-  auto softmax = [&](int tile, f32x16 (&st)[2], V8 (&pf)[4], float& alpha, auto masked_tag) {
-    constexpr bool masked = decltype(masked_tag)::value;
-    // Element i of block mt holds key tile*64 + 32*mt + 8*(i/4) + 4*hi + i%4;
-    // it is visible when that key is <= pos, i.e. when the compile-time part
-    // 32*mt + 8*(i/4) + i%4 is <= lim.  (Comparing against one per-lane limit
-    // keeps 32 per-lane key offsets from being hoisted out of the loop.)
-    const int lim = pos - tile * kPrefillKeys - 4 * hi;
-    float tmax = -INFINITY;
+  // Probabilities of element pair q (elements 2q, 2q + 1 of the 32 a lane
+  // holds), in three stages one step apart so that no stage waits on the
+  // latency of the previous one: (A) the exponents S * scale - m, (B) their
+  // exp2, (C) the packed pair into pw and the row sums.  (Two v_add cost less
+  // than a v_dot2 of the packed pair beside the MFMAs.)
+  // la / lb: this tile's sums of the even / odd elements, added to l once
+  // the tile's last pair is done (the same order as the ping-pong kernel, so
+  // the two kernels agree bit for bit).
+  float px[16][2], pe[16][2], la = 0.f, lb = 0.f;
+  auto pair_a = [&](const f32x16 (&st)[2], int q) {
+    const int mt = q >> 3, i = 2 * (q & 7);
+    px[q][0] = st[mt][i] * p.scale_log2 - m_use;
+    px[q][1] = st[mt][i + 1] * p.scale_log2 - m_use;
+  };
+  auto pair_b = [&](int q) {
+    pe[q][0] = fast_exp2(px[q][0]);
+    pe[q][1] = fast_exp2(px[q][1]);
+  };
+  auto pair_c = [&](u32x4 (&pw)[4], int q) {
+    const int mt = q >> 3, i = 2 * (q & 7);
+    pw[2 * mt + (q & 7) / 4][((i >> 2) & 1) * 2 + ((i & 3) >> 1)] = PackedPair<T>::pack(pe[q][0], pe[q][1]);
+    la += pe[q][0];
+    lb += pe[q][1];
+    if (q == 15) {
+      l += la + lb;
+      la = 0.f;
+      lb = 0.f;
+    }
+  };
+  // Mask and running max of four elements (4c .. 4c + 3) of the next tile's S.
+  auto max4 = [&](f32x16 (&st)[2], int c, int tile, auto masked_tag) {
+    const int mt = c >> 2, i0 = 4 * (c & 3);
+    if constexpr (decltype(masked_tag)::value) {
+      // Key tile*64 + 32*mt + 8*(i/4) + 4*hi + i%4 is visible when
+      // 32*mt + 8*(i/4) + i%4 <= lim.
+      const int lim = pos - tile * kPrefillKeys - 4 * hi;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        if constexpr (masked) {
-          if (32 * mt + 8 * (i >> 2) + (i & 3) > lim) st[mt][i] = -INFINITY;
-        }
-        tmax = fmaxf(tmax, st[mt][i]);
-      }
+      for (int i = i0; i < i0 + 4; ++i)
+        if (32 * mt + 8 * (i >> 2) + (i & 3) > lim) st[mt][i] = -INFINITY;
+    }
+    // IEEE maximum (NaN-propagating, v_maximum3_f32) needs no quieting of
+    // its MFMA-produced inputs, unlike fmaxf.
+    const float m3 = __builtin_elementwise_maximum(__builtin_elementwise_maximum(st[mt][i0], st[mt][i0 + 1]),
+                                                   st[mt][i0 + 2]);
+    tmax = __builtin_elementwise_maximum(__builtin_elementwise_maximum(tmax, m3), st[mt][i0 + 3]);
+    asm volatile("" : "+v"(tmax));  // keeps this part of the max at its step
+  };
+  // Reference-max update from tmax: the max is only moved when it grows by
+  // more than 8 (log2 units), so P stays <= 2^8 and most tiles skip the O
+  // rescale (alpha exactly 1).
+  auto max_update = [&]() {
     const float tmax_s = pair_max(tmax) * p.scale_log2;  // scale > 0 commutes with max
-    // Move the reference max only when it grows by > 8 (p stays <= 2^8).
+    tmax = -INFINITY;
     const bool grow = tmax_s > m + 8.0f;
     const float m_new = grow ? tmax_s : m;
     alpha = grow ? fast_exp2(m - m_new) : 1.0f;  // m = -inf -> 0
     m = m_new;
     l *= alpha;
-    const float m_use = (m == -INFINITY) ? 0.f : m;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float pr = fast_exp2(st[mt][i] * p.scale_log2 - m_use);
-        l += pr;
-        // PV k-step kk = 2*mt + (i/4)/2, slot (i/4 % 2)*4 + i%4.
-        pf[2 * mt + ((i >> 2) >> 1)][((i >> 2) & 1) * 4 + (i & 3)] = (T)pr;
-      }
+    m_use = (m == -INFINITY) ? 0.f : m;
   };
-
-  // PV: A = V^T via transposed LDS reads.  16-lane group a = lane/16 covers
-  // d offset 16*(a&1) of the 32-d tile and keys 4*hi.. of each 8-key block;
-  // supplier lane ti gives row 4*hi + ti/4 at d offset 4*(ti%4).  The reads
-  // for (dt, j) of k-step kk sit at byte dt*1024 + j*512 past block 4*kk.
-  const int ti = lane & 15;
-  const int dgrp = (lane >> 4) & 1;
-  const int vlane_off = (4 * hi + (ti >> 2)) * 64 + (2 * dgrp + ((ti >> 1) & 1)) * 16 + (ti & 1) * 8;
-  auto pv = [&](const lds_u8* vb, const V8 (&pf)[4]) {
+  auto rescale = [&]() {
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const lds_u8* a = vb + vlane_off + 4 * kk * 1024 + dt * 1024;
-        const s16x4 lo = lds_ld_tr16(a);
-        const s16x4 up = lds_ld_tr16(a + 512);
-        const s16x8 both = __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7);
-        o[dt] = Elem<T>::mfma32(__builtin_bit_cast(V8, both), pf[kk], o[dt]);
-      }
+      for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
     }
   };
 
@@ -250,7 +292,7 @@ __device__ __attribute__((always_inline)) inline void prefill_core(const Prefill
     }
   };
 
-  // Prologue: K(0), K(1), V(0) in flight, then S(0).
+  // Prologue: K(0), K(1), V(0) in flight, then S(0) and its max.
   int pg_v = __builtin_amdgcn_readfirstlane(wk.pg1);  // page of V(t+1) at iteration t (= page of K(t+1))
   {
     const int pg0 = __builtin_amdgcn_readfirstlane(wk.pg0);
@@ -262,13 +304,28 @@ __device__ __attribute__((always_inline)) inline void prefill_core(const Prefill
   __builtin_amdgcn_s_waitcnt(kVmcnt0);
   __syncthreads();
   f32x16 st_a[2], st_b[2];  // S(t) lives in st_a for even t, st_b for odd t
-  qk(k0, st_a);
+  {
+    st_a[0] = f32x16{};
+    st_a[1] = f32x16{};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) st_a[j & 1] = Elem<T>::mfma32(kread(k0, j), qf[j >> 1], st_a[j & 1]);
+    const bool masked0 = full_tiles == 0;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      if (masked0) max4(st_a, c, 0, std::true_type{});
+      else max4(st_a, c, 0, std::false_type{});
+    }
+    max_update();
+  }
 
   // Iteration t.  kb_cur holds K(t) (free: S(t) is done) and receives
   // K(t+2); kb_next holds K(t+1); vb_cur holds V(t); vb_next receives V(t+1);
-  // st_cur holds S(t) and st_next receives S(t+1).
+  // st_cur holds S(t), already masked with its max taken, and st_next
+  // receives S(t+1).  Without a next tile (has_next false) the S(t+1) MFMAs
+  // and its max are left out.
   auto iteration = [&](int t, lds_u8* kb_cur, lds_u8* kb_next, lds_u8* vb_cur, lds_u8* vb_next,
-                       f32x16 (&st_cur)[2], f32x16 (&st_next)[2], auto masked_tag) {
+                       f32x16 (&st_cur)[2], f32x16 (&st_next)[2], auto masked_next_tag, auto has_next_tag) {
+    constexpr bool has_next = decltype(has_next_tag)::value;
     __builtin_amdgcn_s_waitcnt(kVmcnt0);
     __syncthreads();  // K(t+1), V(t) landed for all waves; S(t) and PV(t-1) done everywhere
     if (t == ntiles - 1 && (t + 1) * kPrefillKeys > kv) {
@@ -279,35 +336,69 @@ __device__ __attribute__((always_inline)) inline void prefill_core(const Prefill
     if (t + 1 < ntiles) dma_v(pg_v, vb_next);
     pg_v = pg_k;
     pg_k = page_of(t + 3);
-    // S(t+1) on the matrix cores alongside the softmax of S(t).  Past the
-    // last tile this reads a stale buffer and the result is never used.
-    qk(kb_next, st_next);
-    V8 pf[4];
-    float alpha;
-    softmax(t, st_cur, pf, alpha, masked_tag);
-    // alpha is exactly 1 on rows whose max did not move: most tiles skip the
-    // rescale.  (With S(t) and S(t+1) in fixed registers the branch leaves O
-    // in place; a copy of S per tile made the compiler keep two copies of O.)
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+    rescale();  // O *= alpha(t) before P(t) V(t) accumulates
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 32 steps: 0..15 the S(t+1) MFMAs (kread one step ahead), 16..31 the
+    // P(t)V(t) MFMAs (vread one step ahead; k-step kk from step 16 + 4kk).
+    // Pair q of P(t) runs stage A at step (3q)/2, B and C on the two steps
+    // after it, so k-step kk's pairs are packed before step 16 + 4kk; the
+    // mask and max of S(t+1) run on steps 24..31, and its reference-max
+    // update after them.
+    u32x4 pw[4];
+    V8 kf[2], vf[2];
+    if constexpr (has_next) {
+      kf[0] = kread(kb_next, 0);
+      st_next[0] = f32x16{};
+      st_next[1] = f32x16{};
     }
-    pv(vb_cur, pf);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      if (j < 16) {
+        if constexpr (has_next) {
+          if (j + 1 < 16) kf[(j + 1) & 1] = kread(kb_next, j + 1);
+          st_next[j & 1] = Elem<T>::mfma32(kf[j & 1], qf[j >> 1], st_next[j & 1]);
+        }
+        if (j == 15) vf[0] = vread(vb_cur, 0);
+      } else {
+        const int v = j - 16;
+        if (v + 1 < 16) vf[(v + 1) & 1] = vread(vb_cur, v + 1);
+        o[v & 3] = Elem<T>::mfma32(vf[v & 1], __builtin_bit_cast(V8, pw[v >> 2]), o[v & 3]);
+      }
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int sa = (3 * q) >> 1;
+        if (j == sa) pair_a(st_cur, q);
+        if (j == sa + 1) pair_b(q);
+        if (j == sa + 2) pair_c(pw, q);
+      }
+      if constexpr (has_next) {
+        if (j >= 24) max4(st_next, j - 24, t + 1, masked_next_tag);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (has_next) max_update();
   };
 
-  // Tiles below every row's causal bound, then the masked diagonal tiles.
-  // Unrolled by two so each iteration body names its LDS buffers and S
-  // registers statically.
-  auto run = [&](int t, int t_stop, auto masked_tag) {
-    if (t < t_stop && (t & 1)) iteration(t++, k1, k0, v1, v0, st_b, st_a, masked_tag);
+  // Iterations [t, t_stop), each with a next tile, its S masked iff the tag
+  // says so.  Unrolled by two so each iteration body names its LDS buffers
+  // and S registers statically.
+  const std::true_type yes;
+  const std::false_type no;
+  auto run = [&](int t, int t_stop, auto masked_next_tag) {
+    if (t < t_stop && (t & 1)) iteration(t++, k1, k0, v1, v0, st_b, st_a, masked_next_tag, yes);
     for (; t + 1 < t_stop; t += 2) {
-      iteration(t, k0, k1, v0, v1, st_a, st_b, masked_tag);
-      iteration(t + 1, k1, k0, v1, v0, st_b, st_a, masked_tag);
+      iteration(t, k0, k1, v0, v1, st_a, st_b, masked_next_tag, yes);
+      iteration(t + 1, k1, k0, v1, v0, st_b, st_a, masked_next_tag, yes);
     }
-    if (t < t_stop) iteration(t, k0, k1, v0, v1, st_a, st_b, masked_tag);
+    if (t < t_stop) iteration(t, k0, k1, v0, v1, st_a, st_b, masked_next_tag, yes);
   };
-  run(0, full_tiles, std::false_type{});
-  run(full_tiles, ntiles, std::true_type{});
+  // Tile t + 1 is below every row's causal bound iff t + 1 < full_tiles.
+  const int t_split = max(min(full_tiles - 1, ntiles - 1), 0);
+  run(0, t_split, no);
+  run(t_split, ntiles - 1, yes);
+  if ((ntiles - 1) & 1) iteration(ntiles - 1, k1, k0, v1, v0, st_b, st_a, no, no);
+  else iteration(ntiles - 1, k0, k1, v0, v1, st_a, st_b, no, no);
 
   // Epilogue: O^T / l -> out[token][head][d].
   const float l_tot = pair_sum(l);

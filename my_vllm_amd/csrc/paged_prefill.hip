@@ -2,6 +2,7 @@
 // single-launch MIXED kernel (prefill tiles + decode items in one grid).
 #include "mva_capi.h"
 #include "paged_prefill.h"
+#include "paged_prefill_pingpong.h"
 
 namespace mva {
 
@@ -133,35 +134,29 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* __res
 // time it ends, so the grid never waits on dispatch and faster CUs simply
 // run more tiles.
 template <typename T>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void paged_prefill_stream_kernel(
-    PrefillParams p, int32_t* __restrict__ plan) {
-  __shared__ __attribute__((aligned(16))) uint8_t k0[kPrefillTileBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t k1[kPrefillTileBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t v0[kPrefillTileBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t v1[kPrefillTileBytes];
+__global__ __launch_bounds__(kPrefillPPThreads) void paged_prefill_stream_kernel(PrefillParams p,
+                                                                                 int32_t* __restrict__ plan) {
+  __shared__ __attribute__((aligned(16))) uint8_t tiles[kPrefillPPLdsBytes];
   __shared__ int claimed;
   const int h = (int)(blockIdx.x % (uint32_t)p.num_kv_heads);
   const int n = sload(plan, 0);
+  const int slot = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) & 3;
   int* const ctr = plan + kPrefillPlanLineInts * (1 + h);
   auto claim = [&]() { return __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
   if (threadIdx.x == 0) claimed = claim();
   __syncthreads();
   int idx = claimed;
   while (idx < n) {
-    const PrefillWork wk = plan_work(plan, idx);
+    const PrefillWork wk = plan_work_slot(plan, idx, slot);
     int next = 0;
     if (threadIdx.x == 0) next = claim();
-    prefill_core<T>(p, wk, h, (lds_u8*)k0, (lds_u8*)k1, (lds_u8*)v0, (lds_u8*)v1);
+    prefill_core_pingpong<T>(p, wk, h, (lds_u8*)tiles);
     __syncthreads();  // every wave is done with this tile's LDS before `claimed` changes
     if (threadIdx.x == 0) claimed = next;
     __syncthreads();
     idx = claimed;
   }
 }
-
-// Resident workgroups of the persistent prefill per CU (the kernel's
-// registers allow two 256-thread workgroups per CU).
-constexpr int kPrefillStreamGroupsPerCu = 2;
 
 int device_cu_count() {
   static int counts[64] = {};
@@ -308,20 +303,21 @@ extern "C" int mva_paged_prefill(const void* q, int64_t q_token_stride, int64_t 
   hipStream_t s = (hipStream_t)stream;
   int32_t* plan = (int32_t*)workspace;
   if (num_kv_heads > kPrefillPlanMaxHeads) return set_error("paged attention: at most 127 KV heads");
+  p.tile_tokens = kPrefillPPRows / p.group;
   hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(1024), 0, s, query_start_loc, seq_lens, block_tables,
                      block_table_stride, num_pages, (int)num_seqs, p.tile_tokens, num_kv_heads, plan,
                      (int)max_tiles);
   rc = check_launch("paged_prefill plan");
   if (rc) return rc;
-  // Persistent grid: enough workgroups to fill every CU, a whole number per
-  // KV head, never more than the tiles can use.
-  int64_t per_head = (int64_t)kPrefillStreamGroupsPerCu * device_cu_count() / num_kv_heads;
+  // Persistent grid: one workgroup per CU (96 KB of LDS and two waves per
+  // SIMD each), a whole number per KV head, never more than the tiles can use.
+  int64_t per_head = (int64_t)device_cu_count() / num_kv_heads;
   per_head = per_head < 1 ? 1 : (per_head > max_tiles ? max_tiles : per_head);
   const dim3 grid((uint32_t)(per_head * num_kv_heads));
   if (dtype == kBF16)
-    hipLaunchKernelGGL(paged_prefill_stream_kernel<__bf16>, grid, dim3(256), 0, s, p, plan);
+    hipLaunchKernelGGL(paged_prefill_stream_kernel<__bf16>, grid, dim3(kPrefillPPThreads), 0, s, p, plan);
   else
-    hipLaunchKernelGGL(paged_prefill_stream_kernel<_Float16>, grid, dim3(256), 0, s, p, plan);
+    hipLaunchKernelGGL(paged_prefill_stream_kernel<_Float16>, grid, dim3(kPrefillPPThreads), 0, s, p, plan);
   return check_launch("paged_prefill");
 }
 

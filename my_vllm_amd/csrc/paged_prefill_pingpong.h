@@ -1,0 +1,362 @@
+// Ragged causal chunked prefill, ping-pong form: the kernel behind
+// mva_paged_prefill (the PREFILL route).  Same mathematics, LDS tile layouts
+// and MFMA fragment layouts as prefill_core (paged_prefill.h).
+//
+// A workgroup of 8 wavefronts (two per SIMD) holds a 256-row query tile (the
+// G query heads of a KV head x 256 / G tokens, head-major); wave w owns rows
+// 32w .. 32w + 31.  Every wave alternates two kinds of phase per 64-key tile:
+//   M(t): P(t-1) V(t-1) and S(t) = K(t) Q^T on the matrix cores (32 MFMAs and
+//         their LDS fragment reads, almost no vector work);
+//   S(t): the softmax of S(t) on the vector ALU (mask, row max, reference-max
+//         update, O rescale, P(t) = exp2(S * scale - m) packed for the next
+//         M phase, row sums; no MFMA).
+// Waves 0-3 (group 0) run M(0) S(0) M(1) S(1) ... M(n); waves 4-7 (group 1)
+// run the same sequence one phase later, and a workgroup barrier closes
+// every phase.  So each SIMD always holds one wave in an M phase and one in
+// an S phase: the matrix cores of a SIMD overlap the vector work of the
+// other wave, which they do well, instead of that of their own wave, which
+// they do poorly.
+//
+// K and V tiles are triple-buffered in LDS (96 KB).  At even phase 2t the
+// waves of group 0 issue the copies of K(t+2) and those of group 1 the
+// copies of V(t+1), one 16-key page each (4 global_load_lds of 1 KB): the
+// copies have two phase pairs to arrive, which the K/V stream (shared by all
+// workgroups of a head through L2, but larger than L2 for long contexts)
+// needs.
+#pragma once
+
+#include "paged_prefill.h"
+
+namespace mva {
+
+constexpr int kPrefillPPRows = 256;     // query rows per workgroup
+constexpr int kPrefillPPThreads = 512;  // 8 wavefronts
+constexpr int kPrefillPPBufs = 3;       // LDS buffers per K and V
+constexpr int kPrefillPPLdsBytes = 2 * kPrefillPPBufs * kPrefillTileBytes;
+
+// The plan record of tile `idx` with the page ids of page slot `slot` (0..3)
+// of 64-key tiles 0 and 1.
+__device__ inline PrefillWork plan_work_slot(const int32_t* plan, int idx, int slot) {
+  const i32x16 d = ((const_i32x16*)(plan + kPrefillPlanHeaderInts))[idx];
+  PrefillWork wk;
+  wk.s = d[0];
+  wk.t0 = d[1];
+  wk.q0 = d[2];
+  wk.q_len = d[3];
+  wk.kv = d[4];
+  wk.ntiles = d[5];
+  wk.full_tiles = d[6];
+  wk.npages = d[7];
+  wk.pg0 = slot == 0 ? d[8] : slot == 1 ? d[9] : slot == 2 ? d[10] : d[11];
+  wk.pg1 = slot == 0 ? d[12] : slot == 1 ? d[13] : slot == 2 ? d[14] : d[15];
+  return wk;
+}
+
+// One work item.  `tiles` holds kPrefillPPBufs K tile buffers then as many
+// V tile buffers (kPrefillTileBytes each); tile x uses buffer x % kPrefillPPBufs.
+// pg0 / pg1 in wk are this wave's page slot (w % 4) of tiles 0 and 1.
+template <typename T>
+__device__ __attribute__((always_inline)) inline void prefill_core_pingpong(const PrefillParams& p,
+                                                                            const PrefillWork& wk, int h,
+                                                                            lds_u8* tiles) {
+  typedef typename Elem<T>::v8 V8;
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // 0..7
+  const int grp = w >> 2;
+  const int slot = w & 3;  // page slot this wave copies
+  const int lane = tid & 63;
+  const int ln = lane & 31;
+  const int hi = lane >> 5;
+
+  const int s = wk.s;
+  const int t0 = wk.t0;
+  const int q0 = wk.q0;
+  const int q_len = wk.q_len;
+  const int kv = wk.kv;
+  const int G = p.group;
+  const int BMT = p.tile_tokens;  // 256 / G
+  const int base_pos = kv - q_len;
+  const int n = wk.ntiles;
+  const int full_tiles = wk.full_tiles;
+
+  // This lane's query row.
+  const int R = 32 * w + ln;
+  const int g = R / BMT;
+  const int tq = t0 + R % BMT;
+  const bool row_ok = g < G && tq < q_len;
+  const int pos = row_ok ? base_pos + tq : -1;  // keys j <= pos are visible
+
+  V8 qf[8];
+  {
+    const int row_tok = q0 + (row_ok ? tq : 0);
+    const int head = h * G + (g < G ? g : 0);
+    const T* qp = (const T*)p.q + (int64_t)row_tok * p.q_tok_stride + (int64_t)head * p.q_head_stride;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) qf[kk] = row_ok ? ld16<V8>(qp + 8 * (2 * kk + hi)) : V8{};
+  }
+
+  // Copies: group 0 fills K tiles, group 1 V tiles, wave w page slot w % 4.
+  const int32_t* bt = p.block_tables + (int64_t)s * p.bt_stride;
+  const int npages = wk.npages;
+  auto page_of = [&](int tile) {
+    const int pg = sload(bt, min(tile * (kPrefillKeys / kPageSize) + slot, npages - 1));
+    return (pg >= 0 && pg < p.num_pages) ? pg : 0;
+  };
+  const uint32_t koff = (uint32_t)(((lane & 15) * p.tok_stride + 8 * (lane >> 4)) * (int64_t)sizeof(T));
+  const uint32_t voff = (uint32_t)(((lane >> 2) * p.tok_stride + 8 * (lane & 3)) * (int64_t)sizeof(T));
+  auto kbuf = [&](int tile) { return tiles + (tile % kPrefillPPBufs) * kPrefillTileBytes; };
+  auto vbuf = [&](int tile) { return tiles + (kPrefillPPBufs + tile % kPrefillPPBufs) * kPrefillTileBytes; };
+  // The group is a compile-time constant here: a run-time choice between the
+  // K and V cache pointers would make the compiler index the kernel argument
+  // block and copy it to scratch.
+  auto copy_page = [&](int tile, int page, auto grp_tag) __attribute__((always_inline)) {
+    constexpr int kGrp = decltype(grp_tag)::value;
+    const T* src = (const T*)(kGrp == 0 ? p.k_cache : p.v_cache) + h * kHeadDim;
+    lds_u8* buf = kGrp == 0 ? kbuf(tile) : vbuf(tile);
+    dma16_x4_saddr(src + (int64_t)__builtin_amdgcn_readfirstlane(page) * p.page_stride, kGrp == 0 ? koff : voff,
+                   (uint32_t)(uintptr_t)(buf + 4096 * slot));
+  };
+
+  // Fragment reads (layouts as in prefill_core).
+  auto kread = [&](const lds_u8* kb, int j) {  // QK step j: chain j % 2, k-step j / 2
+    return lds_ld16<V8>(kb + klds_off(32 * (j & 1) + ln, 2 * (j >> 1) + hi));
+  };
+  const int ti = lane & 15;
+  const int dgrp = (lane >> 4) & 1;
+  const int vlane_off = (4 * hi + (ti >> 2)) * 64 + (2 * dgrp + ((ti >> 1) & 1)) * 16 + (ti & 1) * 8;
+  auto vread = [&](const lds_u8* vb, int j) {  // PV step j: k-step j / 4, d-tile j % 4
+    const lds_u8* a = vb + vlane_off + (j >> 2) * 4096 + (j & 3) * 1024;
+    return __builtin_bit_cast(V8, __builtin_shufflevector(lds_ld_tr16(a), lds_ld_tr16(a + 512), 0, 1, 2, 3, 4, 5, 6,
+                                                          7));
+  };
+
+  f32x16 o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{};
+  f32x16 st[2];  // S(t): st[mt][i] = S[query ln][key 32*mt + 8*(i/4) + 4*hi + i%4]
+  u32x4 pw[4];   // P(t) for PV k-step kk: four packed pairs
+  float m = -INFINITY;  // reference max (log2 units) of the tiles so far
+  float l = 0.f;        // row sum of P relative to m
+
+  // Phase fences for the compiler.  A barrier orders memory only: without
+  // these, passes before instruction scheduling move register-only work (a
+  // row max, the exponentials) across it into the other phase.  An empty
+  // asm statement that "rewrites" a phase's inputs at its start and its
+  // outputs at its end ties that work to its phase.
+  auto pin_s = [&]() __attribute__((always_inline)) { asm volatile("" : "+v"(st[0]), "+v"(st[1])); };
+  auto pin_p = [&]() __attribute__((always_inline)) {
+    asm volatile("" : "+v"(pw[0]), "+v"(pw[1]), "+v"(pw[2]), "+v"(pw[3]));
+  };
+  auto pin_o = [&]() __attribute__((always_inline)) {
+    asm volatile("" : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]));
+  };
+
+  // M phase t: PV(t-1) and QK(t), alternating, fragment reads one step ahead.
+  auto phase_m = [&](int t, auto with_qk_tag, auto with_pv_tag) __attribute__((always_inline)) {
+    constexpr bool with_qk = decltype(with_qk_tag)::value;
+    constexpr bool with_pv = decltype(with_pv_tag)::value;
+    if constexpr (with_pv) pin_p();
+    const lds_u8* kb = kbuf(t);
+    const lds_u8* vb = vbuf(t + kPrefillPPBufs - 1);  // V(t-1)
+    V8 kf[2], vf[2];
+    if constexpr (with_qk) {
+      kf[0] = kread(kb, 0);
+      st[0] = f32x16{};
+      st[1] = f32x16{};
+    }
+    if constexpr (with_pv) vf[0] = vread(vb, 0);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      if constexpr (with_qk) {
+        if (j + 1 < 16) kf[(j + 1) & 1] = kread(kb, j + 1);
+        st[j & 1] = Elem<T>::mfma32(kf[j & 1], qf[j >> 1], st[j & 1]);
+      }
+      if constexpr (with_pv) {
+        if (j + 1 < 16) vf[(j + 1) & 1] = vread(vb, j + 1);
+        o[j & 3] = Elem<T>::mfma32(vf[j & 1], __builtin_bit_cast(V8, pw[j >> 2]), o[j & 3]);
+      }
+      // Keeps the fragment reads one step ahead instead of all at the top,
+      // which would hold 48 fragments in registers at once.
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (with_qk) pin_s();
+    if constexpr (with_pv) pin_o();
+  };
+
+  // S phase t: softmax of S(t) into P(t).
+  auto phase_s = [&](int t) __attribute__((always_inline)) {
+    pin_s();
+    if (t >= full_tiles) {
+      // Key t*64 + 32*mt + 8*(i/4) + 4*hi + i%4 is visible when
+      // 32*mt + 8*(i/4) + i%4 <= lim.  lim and S pass through an empty asm
+      // statement so that the compares and selects stay inside this branch:
+      // hoisted, they would run on every tile and hold 32 compare masks in
+      // scalar registers.
+      int lim = pos - t * kPrefillKeys - 4 * hi;
+      asm volatile("" : "+v"(lim), "+v"(st[0]), "+v"(st[1]));
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (32 * mt + 8 * (i >> 2) + (i & 3) > lim) st[mt][i] = -INFINITY;
+    }
+    // Row max with the IEEE maximum (v_maximum3_f32), which needs no quieting
+    // of MFMA-produced inputs, unlike fmaxf.
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; i += 2)
+        tmax = __builtin_elementwise_maximum(__builtin_elementwise_maximum(tmax, st[mt][i]), st[mt][i + 1]);
+    // The reference max moves only when it grows by more than 8 (log2
+    // units): P stays <= 2^8 and most tiles skip the O rescale.
+    const float tmax_s = pair_max(tmax) * p.scale_log2;  // scale > 0 commutes with max
+    const bool grow = tmax_s > m + 8.0f;
+    const float m_new = grow ? tmax_s : m;
+    const float alpha = grow ? fast_exp2(m - m_new) : 1.0f;  // m = -inf -> 0
+    m = m_new;
+    const float m_use = (m == -INFINITY) ? 0.f : m;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+      l *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+    }
+    float la = 0.f, lb = 0.f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {  // element pair q: elements 2q, 2q + 1
+      const int mt = q >> 3, i = 2 * (q & 7);
+      const float e0 = fast_exp2(st[mt][i] * p.scale_log2 - m_use);
+      const float e1 = fast_exp2(st[mt][i + 1] * p.scale_log2 - m_use);
+      pw[2 * mt + (q & 7) / 4][((i >> 2) & 1) * 2 + ((i & 3) >> 1)] = PackedPair<T>::pack(e0, e1);
+      la += e0;
+      lb += e1;
+    }
+    l += la + lb;
+    pin_p();
+  };
+
+  // Zero V rows of keys >= kv in the last tile (stale rows may hold NaN and
+  // 0 * NaN would leak through P = 0).
+  auto zero_tail = [&](int tile) __attribute__((always_inline)) {
+    lds_u8* vb = vbuf(tile);
+    const int first_bad = kv - tile * kPrefillKeys;  // rows >= first_bad are past the sequence
+    for (int i = tid; i < (kPrefillKeys - first_bad) * 16; i += kPrefillPPThreads) {
+      const int key = first_bad + (i >> 4);
+      lds_st16<u32x4>(vb + vlds_blk_off(key, i & 15), u32x4{0, 0, 0, 0});
+    }
+  };
+
+  const std::true_type yes;
+  const std::false_type no;
+  // A workgroup barrier that also closes the phase for the instruction
+  // scheduler (s_barrier alone lets register-only work move across it).
+  auto phase_barrier = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Prologue: K(0), K(1) (group 0) and V(0) (group 1) resident before
+  // phase 0.
+  if (grp == 0) {
+    copy_page(0, wk.pg0, std::integral_constant<int, 0>{});
+    if (1 < n) copy_page(1, wk.pg1, std::integral_constant<int, 0>{});
+  } else {
+    copy_page(0, wk.pg0, std::integral_constant<int, 1>{});
+  }
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);
+  phase_barrier();
+
+  // Phases 0 .. 2n+1.  At phase 2t group 0 copies K(t+2) and group 1 V(t+1)
+  // (three buffers each: the buffer written was last read in phase 2t-1),
+  // and every wave waits for its copies of phase 2t-2 at the end of phase
+  // 2t+1, before the barrier that opens their first reader's phase 2t+2; so
+  // a copy has two phase pairs to land.  pg_next is the page id of this
+  // wave's next copy; it is loaded at the start of an S phase (no LDS reads
+  // there to wait behind the scalar load) and used at the next even phase.
+  // V(n-1) lands by the end of phase 2n-1 and is first read in phase 2n
+  // (group 0's M(n)): its stale tail rows are cleared between them.  Both
+  // groups pass the same barriers.  Each group runs its own copy of the
+  // schedule (the group is a compile-time constant inside), so no value has
+  // to meet in the same registers on both groups' paths, and M(0) (no PV)
+  // and M(n) (no QK) are peeled off the loop so the loop body holds one copy
+  // of each phase.
+  const bool tail = n * kPrefillKeys > kv;
+  // End of phase 2t+1; `issued` says whether this wave copied at phase 2t
+  // (those 4 copies may stay in flight; vmcnt counts in issue order).
+  auto end_odd_phase = [&](int t, bool issued) __attribute__((always_inline)) {
+    if (issued) __builtin_amdgcn_s_waitcnt(waitcnt_vm(4));
+    else __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    phase_barrier();
+    if (t == n - 1 && tail) {
+      zero_tail(n - 1);
+      phase_barrier();
+    }
+  };
+  auto run = [&](auto grp_tag) __attribute__((always_inline)) {
+    constexpr int kGrp = decltype(grp_tag)::value;
+    // Tile copied at phase 2t: c(t) = t + 2 (K) or t + 1 (V).
+    constexpr int kAhead = kGrp == 0 ? 2 : 1;
+    int pg_next = kGrp == 0 ? page_of(2) : __builtin_amdgcn_readfirstlane(wk.pg1);
+    // Phases 0 and 1.
+    const bool issued0 = kAhead < n;
+    if (issued0) copy_page(kAhead, pg_next, grp_tag);
+    if constexpr (kGrp == 0) {
+      phase_m(0, yes, no);
+      phase_barrier();
+      pg_next = page_of(3);
+      phase_s(0);
+    } else {
+      pg_next = page_of(2);
+      phase_barrier();
+      phase_m(0, yes, no);
+    }
+    end_odd_phase(0, issued0);
+    // Phases 2t and 2t+1, t = 1 .. n-1.
+    for (int t = 1; t < n; ++t) {
+      const bool issued = t + kAhead < n;
+      if (issued) copy_page(t + kAhead, pg_next, grp_tag);
+      if constexpr (kGrp == 0) {
+        phase_m(t, yes, yes);
+        phase_barrier();
+        pg_next = page_of(t + 3);
+        phase_s(t);
+      } else {
+        pg_next = page_of(t + 2);
+        phase_s(t - 1);
+        phase_barrier();
+        phase_m(t, yes, yes);
+      }
+      end_odd_phase(t, issued);
+    }
+    // Phases 2n and 2n+1.
+    if constexpr (kGrp == 0) {
+      phase_m(n, no, yes);
+      phase_barrier();
+    } else {
+      phase_s(n - 1);
+      phase_barrier();
+      phase_m(n, no, yes);
+    }
+    phase_barrier();
+  };
+  if (grp == 0) run(std::integral_constant<int, 0>{});
+  else run(std::integral_constant<int, 1>{});
+
+  // Epilogue: O^T / l -> out[token][head][d].
+  const float l_tot = pair_sum(l);
+  if (!row_ok) return;
+  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  T* op = (T*)p.out + (int64_t)(q0 + tq) * p.out_tok_stride + (int64_t)(h * G + g) * p.out_head_stride;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int bk = 0; bk < 4; ++bk) {
+      typename Elem<T>::v4 wv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wv[e] = (T)(o[dt][4 * bk + e] * inv);
+      *reinterpret_cast<typename Elem<T>::v4*>(op + 32 * dt + 8 * bk + 4 * hi) = wv;
+    }
+}
+
+}  // namespace mva

@@ -19,6 +19,9 @@ DECODE_ITEM_INTS = 8
 MAX_CHUNK_PAGES = 128
 # Query rows per prefill workgroup (kPrefillRows): G heads x 128 // G tokens.
 PREFILL_ROWS = 128
+# Query rows per tile of mva_paged_prefill's kernel (the MIXED kernel's
+# prefill tiles have PREFILL_ROWS).
+PREFILL_STREAM_ROWS = 256
 # int32 fields per prefill work item of the MIXED launch (kPrefillItemInts).
 PREFILL_ITEM_INTS = 4
 # Device-built prefill tile list: header ints (tile count + per-head claim
@@ -536,7 +539,7 @@ def _tail_args(q, k_cache, softmax_scale):
 def prefill_max_tiles(num_prefill_tokens: int, num_prefill_seqs: int, num_q_heads: int, num_kv_heads: int) -> int:
     """Bound on the query tiles of a prefill batch: sum(ceil(q_s / tile)) <=
     tokens // tile + sequences."""
-    tile = PREFILL_ROWS // (num_q_heads // num_kv_heads)
+    tile = PREFILL_STREAM_ROWS // (num_q_heads // num_kv_heads)
     return num_prefill_tokens // tile + num_prefill_seqs
 
 

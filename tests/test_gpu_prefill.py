@@ -220,7 +220,7 @@ def test_device_tile_plan_is_exact(gpu, hq, hkv):
     backend.forward(qd, empty, empty, kc, vc, p)
     torch.cuda.synchronize()
     backend_ws = backend._prefill_workspace.view(torch.int32).cpu()
-    tile = 128 // (hq // hkv)
+    tile = ops.PREFILL_STREAM_ROWS // (hq // hkv)
     want = _expected_tiles(q, kv, tile)
     assert int(backend_ws[0]) == len(want) <= p.metadata.prefill_max_tiles
     head, rec = ops.PREFILL_PLAN_HEADER_INTS, ops.PREFILL_PLAN_ITEM_INTS
