@@ -295,15 +295,6 @@ def extra_measurements(device, steps: int):
         empty = q.new_empty((0, hkv, 128))
         return time_launches(lambda i: backend.forward(q, empty, empty, kc, vc, plan), iters, 3)
 
-    # Context for the MFMA-bound figures: the vendor library's dense bf16 GEMM
-    # on N(0,1) operands.  The chip holds lower clocks under dense MFMA work
-    # on real data than the 2.5 PFLOP/s peak assumes.
-    ga = _randn_rows(8192, 8192, seed=30, device=device, rng_device="cuda")
-    gb = _randn_rows(8192, 8192, seed=31, device=device, rng_device="cuda")
-    ms = time_launches(lambda i: torch.matmul(ga, gb), 30, 5)
-    res["gemm_8192_bf16_TFLOPs"] = round(2 * 8192**3 / ms / 1e9, 1)
-    del ga, gb
-
     # PURE_PREFILL with prefix, Qwen3-8B.
     # The same CPU-seeded draw the parity tests check.
     batch = config_prefill(seed=2, device=device)
@@ -328,6 +319,16 @@ def extra_measurements(device, steps: int):
     res["mixed_split_ms"] = round(ms_s, 4)
     res["mixed_unified_roofline_frac"] = round(bound_ms / ms_u, 4)
     del batch
+
+    # Context for the MFMA-bound figures: the vendor library's dense bf16 GEMM
+    # on N(0,1) operands.  The chip holds lower clocks under dense MFMA work
+    # on real data than the 2.5 PFLOP/s peak assumes.  Run after the attention
+    # cases: its heat would lower their clocks.
+    ga = _randn_rows(8192, 8192, seed=30, device=device, rng_device="cuda")
+    gb = _randn_rows(8192, 8192, seed=31, device=device, rng_device="cuda")
+    ms = time_launches(lambda i: torch.matmul(ga, gb), 30, 5)
+    res["gemm_8192_bf16_TFLOPs"] = round(2 * 8192**3 / ms / 1e9, 1)
+    del ga, gb
 
     res.update(graph_vs_eager(device))
 

@@ -279,8 +279,9 @@ int mva_paged_decode_noalloc(const void* q, int64_t q_token_stride, int64_t q_he
                              int64_t out_head_stride, int num_q_heads, int num_kv_heads, int head_dim,
                              int page_size, float softmax_scale, int dtype, void* stream);
 
-/* Query-token rows per prefill workgroup tile for a GQA ratio (128 / ratio),
- * or -1 for invalid head counts. */
+/* Query tokens per prefill tile of mva_paged_mixed for a GQA ratio
+ * (128 / ratio: 128 query rows), or -1 for invalid head counts.
+ * mva_paged_prefill's tiles hold twice as many (256 query rows). */
 int mva_prefill_tile_tokens(int num_q_heads, int num_kv_heads);
 
 /* Bytes of the prefill workspace (the device-built tile list) for at most
@@ -295,13 +296,14 @@ int64_t mva_prefill_workspace_bytes(int64_t max_tiles);
  * tokens' K/V are read from the cache (store them first).
  * The work list is built on the device from query_start_loc and seq_lens
  * (nothing is read back to the host): one query tile per
- * mva_prefill_tile_tokens() tokens x all query heads of a KV head, longest
- * context first, written into `workspace` (mva_prefill_workspace_bytes(
- * max_tiles) bytes, 16-byte aligned).  max_tiles must bound the tile count,
- * e.g. num_prefill_tokens / tile_tokens + num_seqs; tiles beyond it are not
- * run.  A sequence with no queries, or more queries than keys, is skipped.
- * A persistent grid of workgroups then streams the tiles.  Launches that
- * share a workspace must not overlap.
+ * 2 * mva_prefill_tile_tokens() tokens x all query heads of a KV head (256
+ * query rows), longest context first, written into `workspace`
+ * (mva_prefill_workspace_bytes(max_tiles) bytes, 16-byte aligned).
+ * max_tiles must bound the tile count, e.g. num_prefill_tokens / tile_tokens
+ * + num_seqs with tile_tokens = 2 * mva_prefill_tile_tokens(); tiles beyond
+ * it are not run.  A sequence with no queries, or more queries than keys, is
+ * skipped.  A persistent grid of 512-thread workgroups, one per CU, then
+ * streams the tiles.  Launches that share a workspace must not overlap.
  * Replaces FlashInfer BatchPrefillWithPagedKVCacheWrapper.plan/run on the
  * reference's PREFILL route (nanovllm/layers/attention_backend.py:810-825,
  * :992-994) and the prefill half of MIXED_SPLIT (:858-873, :1015-1019).
