@@ -319,11 +319,16 @@ int mva_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_stri
 
 /*
  * MIXED batch in one launch: prefill tiles write the rows of the leading
- * prefill sequences and decode pieces (as mva_paged_decode) write the
- * trailing decode rows of the same `out` buffer.
- *   prefill_items [num_prefill_items, 4] int32 query tiles {seq, first_token,
- *         0, 0} (mva_prefill_tile_tokens() tokens each); tiles past a
- *         sequence's query count exit without writing.
+ * num_prefill_seqs (<= 1024) sequences and decode pieces (as
+ * mva_paged_decode, claim schedule) write the trailing decode rows of the
+ * same `out` buffer.  The prefill tiles (mva_prefill_tile_tokens() tokens
+ * x the query heads of a KV head: 128 query rows) are derived on the device
+ * from query_start_loc and seq_lens, longest context first, and run by a
+ * persistent pool of prefill workgroups; max_prefill_tiles bounds their
+ * number (num_prefill_tokens / tile_tokens + num_prefill_seqs) and only
+ * sizes the pool.  The workspace (mva_decode_workspace_bytes) also holds the
+ * pool's claim counters, which the launch leaves at zero.  At most 64 KV
+ * heads when prefill sequences are present.
  * Replaces FlashInfer BatchAttention.plan/run on the reference's MIXED_UNIFIED
  * route (nanovllm/layers/attention_backend.py:841-857, :998-1009).
  */
@@ -331,9 +336,8 @@ int mva_paged_mixed(const void* q, int64_t q_token_stride, int64_t q_head_stride
                     const void* k_cache, const void* v_cache, int64_t num_pages,
                     int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
                     int64_t block_table_stride, const int32_t* seq_lens,
-                    const int32_t* query_start_loc, const int32_t* prefill_items,
-                    int64_t num_prefill_items, const int32_t* decode_items,
-                    int64_t num_decode_items, int64_t num_decode_waves,
+                    const int32_t* query_start_loc, int64_t num_prefill_seqs, int64_t max_prefill_tiles,
+                    const int32_t* decode_items, int64_t num_decode_items, int64_t num_decode_waves,
                     const int32_t* decode_merges, int64_t num_decode_merges, int64_t num_part_slots,
                     void* out, int64_t out_token_stride, int64_t out_head_stride,
                     void* workspace, int64_t workspace_bytes, int num_q_heads, int num_kv_heads,

@@ -133,7 +133,7 @@ _SIGNATURES = {
             _c_void_p, _i64, _i64,
             _c_void_p, _c_void_p, _i64, _i64, _i64,
             _c_void_p, _i64, _c_void_p, _c_void_p,
-            _c_void_p, _i64, _c_void_p, _i64, _i64,  # prefill items, decode items, waves
+            _i64, _i64, _c_void_p, _i64, _i64,  # prefill seqs, max prefill tiles, decode items, waves
             _c_void_p, _i64, _i64,  # decode merges, num merges, num_part_slots
             _c_void_p, _i64, _i64,
             _c_void_p, _i64,
@@ -144,7 +144,7 @@ _SIGNATURES = {
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 # The C ABI revision these signatures describe (mva_abi_version()).
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -66,10 +66,12 @@ class MI355XAttentionMetadata:
     runs its own piece list (``make_decode_plan_listed``); without it the
     wavefronts claim pieces (``make_decode_plan``).  ``decode_merges`` lists the split segments
     (``ops.decode_merge_list``) whose partials the merge kernel combines.
-    ``prefill_items`` is int32 ``[num_prefill_items, 4]`` query tiles of the
-    single MIXED launch (see ``make_prefill_items``); the PREFILL and split
-    routes plan their tiles on the device, within ``prefill_max_tiles``.  ``kv_indptr`` is the page CSR offset list (host
-    ints): sequence ``s`` owns pages ``block_tables[s, :kv_indptr[s+1]-kv_indptr[s]]``.
+    Prefill query tiles are derived on the device from ``query_start_loc``
+    and ``seq_lens``: ``prefill_max_tiles`` bounds those of the PREFILL and
+    split routes (256-row tiles), ``mixed_prefill_max_tiles`` those of the
+    single MIXED launch (128-row tiles).  ``kv_indptr`` is the page CSR
+    offset list (host ints): sequence ``s`` owns pages
+    ``block_tables[s, :kv_indptr[s+1]-kv_indptr[s]]``.
     """
 
     query_start_loc: torch.Tensor
@@ -88,10 +90,12 @@ class MI355XAttentionMetadata:
     decode_waves_per_group: int = 1
     # Host copy of a piece-list plan: (items, wave_extra, merges, workgroups).
     decode_host_plan: tuple | None = None
-    prefill_items: torch.Tensor | None = None
-    num_prefill_items: int = 0
-    # Bound on the prefill query tiles (sizes the device-built tile list).
+    # Bounds on the prefill query tiles (size the device-built tile list and
+    # the MIXED launch's prefill pool).  mixed_prefill_max_tiles == 0 on a
+    # MIXED_UNIFIED plan: more prefill sequences or KV heads than one MIXED
+    # launch takes, so the batch runs as prefill + decode launches.
     prefill_max_tiles: int = 0
+    mixed_prefill_max_tiles: int = 0
 
     @property
     def is_cacheless(self) -> bool:
@@ -295,39 +299,6 @@ def make_decode_plan_listed(
     items = np.concatenate([pieces[first], pieces[~is_first]])
     wave_extra = waves + np.concatenate(([0], np.cumsum(per_wave - 1)))
     return items, wave_extra.astype(np.int32), waves, int(split.sum())
-
-
-def make_prefill_items(
-    query_upper: np.ndarray | list[int],
-    kv_upper: np.ndarray | list[int],
-    tile_tokens: int,
-) -> np.ndarray:
-    """Query tiles ``(seq, first_token, 0, 0)`` for prefill sequences ``0..S-1``.
-
-    ``query_upper[s]`` bounds the sequence's new-token count (exact when known;
-    tiles past the real count exit on the device) and ``kv_upper[s]`` its
-    context length.  Tiles are grouped by sequence, longest context first, and
-    within a sequence ordered by their key count, largest first.  Grouping
-    keeps the tiles that read one sequence's K/V in flight together, so
-    those pages are served from L2 instead of being refetched for tiles of
-    many sequences at once; longest-first keeps the launch's tail short.
-    """
-    q_ub = np.asarray(query_upper, dtype=np.int64)
-    kv_ub = np.asarray(kv_upper, dtype=np.int64)
-    ntiles = np.maximum((q_ub + tile_tokens - 1) // tile_tokens, 1)
-    seq = np.repeat(np.arange(q_ub.size), ntiles)
-    first_tile = np.cumsum(ntiles) - ntiles
-    tile = np.arange(int(ntiles.sum())) - np.repeat(first_tile, ntiles)
-    start = tile * tile_tokens
-    end = np.minimum(start + tile_tokens, np.repeat(q_ub, ntiles))
-    cost = np.repeat(kv_ub - q_ub, ntiles) + end
-    items = np.zeros((seq.size, ops.PREFILL_ITEM_INTS), dtype=np.int32)
-    items[:, 0] = seq
-    items[:, 1] = start
-    # Primary key: the sequence's context (longest first, ties by index);
-    # secondary: the tile's key count (largest first).
-    order = np.lexsort((-cost, seq, -kv_ub[seq]))
-    return items[order]
 
 
 def _to_device(array: np.ndarray, device: torch.device) -> torch.Tensor:
@@ -581,7 +552,7 @@ class MI355XAttentionBackendMixin:
         waves_per_group = 1
         if common.num_decode_seqs:
             decode_counts = counts[common.num_prefill_seqs:]
-            one_launch = bool(common.num_prefill_seqs) and self.attention_mode == "unified"
+            one_launch = bool(common.num_prefill_seqs) and self._mixed_in_one_launch(common)
             wave_extra = None
             if not one_launch and decode_schedule(int(decode_counts.sum()), self.num_kv_heads) == "listed":
                 groups, waves_per_group = listed_decode_groups(self.num_kv_heads, block_tables.device)
@@ -612,32 +583,15 @@ class MI355XAttentionBackendMixin:
             if wave_extra is not None:
                 decode_wave_extra = flat[n_items + n_merge:]
                 decode_host_plan = (items, wave_extra, merges, groups)
-        prefill_items = None
-        num_prefill_items = 0
         prefill_max_tiles = 0
+        mixed_prefill_max_tiles = 0
         if common.num_prefill_seqs:
             prefill_max_tiles = ops.prefill_max_tiles(common.num_prefill_tokens, common.num_prefill_seqs,
                                                       self.num_q_heads, self.num_kv_heads)
-        if common.num_prefill_seqs and common.num_decode_seqs and self.attention_mode == "unified":
-            # The single MIXED launch takes host-built tiles; PREFILL and the
-            # split route plan their tiles on the device.
-            num_prefill = common.num_prefill_seqs
-            kv_ub = counts[:num_prefill] * self.block_size
-            if common.trusted:
-                # Only host ints are available: bound each sequence's query count.
-                q_ub = np.minimum(
-                    np.minimum(kv_ub, common.max_q_len),
-                    common.num_prefill_tokens - (num_prefill - 1),
+            if common.num_decode_seqs and self._mixed_in_one_launch(common):
+                mixed_prefill_max_tiles = ops.mixed_prefill_max_tiles(
+                    common.num_prefill_tokens, common.num_prefill_seqs, self.num_q_heads, self.num_kv_heads
                 )
-                q_ub = np.maximum(q_ub, 1)
-            else:
-                qsl = common.query_start_loc[: num_prefill + 1].cpu().numpy().astype(np.int64)
-                q_ub = qsl[1:] - qsl[:-1]
-                kv_ub = common.seq_lens[:num_prefill].cpu().numpy().astype(np.int64)
-            tile_tokens = ops.PREFILL_ROWS // (self.num_q_heads // self.num_kv_heads)
-            items = make_prefill_items(q_ub, kv_ub, tile_tokens)
-            num_prefill_items = items.shape[0]
-            prefill_items = _to_device(items, block_tables.device)
         return MI355XAttentionMetadata(
             query_start_loc=common.query_start_loc,
             seq_lens=common.seq_lens,
@@ -654,9 +608,17 @@ class MI355XAttentionBackendMixin:
             decode_wave_extra=decode_wave_extra,
             decode_waves_per_group=waves_per_group,
             decode_host_plan=decode_host_plan,
-            prefill_items=prefill_items,
-            num_prefill_items=num_prefill_items,
             prefill_max_tiles=prefill_max_tiles,
+            mixed_prefill_max_tiles=mixed_prefill_max_tiles,
+        )
+
+    def _mixed_in_one_launch(self, common) -> bool:
+        """Unified mode runs a MIXED batch as one launch within that launch's
+        limits (prefill sequences, KV heads), else as prefill + decode."""
+        return (
+            self.attention_mode == "unified"
+            and common.num_prefill_seqs <= ops.MIXED_PREFILL_SEQS_MAX
+            and self.num_kv_heads <= ops.MIXED_MAX_KV_HEADS
         )
 
     def build_plan(self, common, metadata: MI355XAttentionMetadata | None = None):
@@ -822,7 +784,7 @@ class MI355XAttentionBackendMixin:
         if route is Route.PREFILL:
             self._run_prefill(q, k_cache, v_cache, common, metadata, output)
             return output
-        if route is Route.MIXED_SPLIT:
+        if route is Route.MIXED_SPLIT or metadata.mixed_prefill_max_tiles == 0:
             if common.num_prefill_seqs:
                 self._run_prefill(q, k_cache, v_cache, common, metadata, output)
             if common.num_decode_seqs:
@@ -1064,8 +1026,8 @@ class MI355XAttentionBackendMixin:
             metadata.block_tables,
             metadata.seq_lens,
             metadata.query_start_loc,
-            metadata.prefill_items,
-            metadata.num_prefill_items,
+            common.num_prefill_seqs,
+            metadata.mixed_prefill_max_tiles,
             metadata.decode_items,
             metadata.num_decode_items,
             metadata.num_decode_waves,
@@ -1120,6 +1082,5 @@ __all__ = [
     "integrate",
     "make_decode_plan",
     "make_decode_plan_listed",
-    "make_prefill_items",
     "resident_decode_waves",
 ]

@@ -271,13 +271,23 @@ __device__ inline void store8_untracked(void* addr, u32x2 v) {
 // 128-byte line (atomics to one line serialize), then the exit counter.
 constexpr int kDecodeClaimCounters = 32;
 constexpr int kDecodeSchedLineInts = 32;
-constexpr int kDecodeSchedBytes = 4352;  // (32 + 1) lines of 128 bytes, rounded up to 256
+// (32 + 2 + kMixedPrefillMaxHeads) lines of 128 bytes, rounded up to 256.
+constexpr int kMixedPrefillMaxHeads = 64;
+constexpr int kDecodeSchedBytes = 12544;
 static_assert((kDecodeClaimCounters + 1) * kDecodeSchedLineInts * 4 <= kDecodeSchedBytes, "sched area");
 // Word set to 1 by a fused-store launch that found a new row whose slot is
 // not in its sequence's last page (the row is not written); on its own line
 // after the exit counter.  Only the host clears it.
 constexpr int kDecodeStoreErrorInt = (kDecodeClaimCounters + 1) * kDecodeSchedLineInts;
 static_assert((kDecodeStoreErrorInt + 1) * 4 <= kDecodeSchedBytes, "store error word");
+// MIXED launches: the prefill claim counter of KV head h at word
+// kMixedPrefillCtrInt + h * kDecodeSchedLineInts and that head's exit
+// counter kMixedPrefillExitOffset words after it; the last prefill
+// workgroup of the head to exit clears both.
+constexpr int kMixedPrefillCtrInt = (kDecodeClaimCounters + 2) * kDecodeSchedLineInts;
+constexpr int kMixedPrefillExitOffset = 16;
+static_assert((kMixedPrefillCtrInt + kMixedPrefillMaxHeads * kDecodeSchedLineInts) * 4 <= kDecodeSchedBytes,
+              "MIXED prefill counters");
 
 // One wavefront of a decode launch (`wave` in [0, num_waves)); `lds` is its
 // kDecodeWaveLdsBytes of LDS.

@@ -38,7 +38,6 @@ namespace mva {
 constexpr int kPrefillRows = 128;  // query rows per workgroup
 constexpr int kPrefillKeys = 64;   // keys per LDS tile
 constexpr int kPrefillTileBytes = kPrefillKeys * kHeadDim * 2;  // one K (or V) tile
-constexpr int kPrefillItemInts = 4;  // {seq, first token of the tile, 0, 0}
 
 struct PrefillParams {
   const void* q;
@@ -53,8 +52,7 @@ struct PrefillParams {
   int64_t bt_stride;
   const int32_t* seq_lens;
   const int32_t* query_start_loc;
-  const int32_t* items;
-  int num_items;
+  int num_seqs;  // prefill sequences (the leading rows of the batch)
   void* out;
   int64_t out_tok_stride;
   int64_t out_head_stride;
@@ -439,56 +437,10 @@ constexpr int kPrefillPlanHeaderInts = kPrefillPlanLineInts * (1 + kPrefillPlanM
 // batch order).
 constexpr int kPrefillPlanSortMax = 2048;
 
-// A work item of the host-built list {seq, t0, 0, 0}: its query count, keys
-// and first pages are read here (tiles past the sequence's queries exit).
-template <typename T>
-__device__ __attribute__((always_inline)) inline void prefill_item(
-    const PrefillParams& p, const int32_t* __restrict__ it, int h, lds_u8* k0, lds_u8* k1, lds_u8* v0,
-    lds_u8* v1) {
-  PrefillWork wk;
-  wk.s = it[0];
-  wk.t0 = it[1];
-  wk.q0 = p.query_start_loc[wk.s];
-  wk.q_len = p.query_start_loc[wk.s + 1] - wk.q0;
-  if (wk.t0 >= wk.q_len) return;  // tile past this sequence's queries (host sizes conservatively)
-  wk.kv = p.seq_lens[wk.s];
-  const int base_pos = wk.kv - wk.q_len;
-  const int kv_end = base_pos + min(wk.t0 + p.tile_tokens, wk.q_len);  // keys [0, kv_end) are needed
-  wk.ntiles = (kv_end + kPrefillKeys - 1) / kPrefillKeys;
-  wk.full_tiles = min((base_pos + wk.t0 + 1) / kPrefillKeys, wk.ntiles);
-  wk.npages = (kv_end + kPageSize - 1) / kPageSize;
-  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-  const int32_t* bt = p.block_tables + (int64_t)wk.s * p.bt_stride;
-  auto page = [&](int i) {
-    const int pg = sload(bt, min(i, wk.npages - 1));
-    return (pg >= 0 && pg < p.num_pages) ? pg : 0;
-  };
-  wk.pg0 = page(w);
-  wk.pg1 = page(kPrefillKeys / kPageSize + w);
-  prefill_core<T>(p, wk, h, k0, k1, v0, v1);
-}
-
 // The tile list mva_paged_prefill builds on the device: the record of tile
 // i at word kPrefillPlanHeaderInts + i * kPrefillPlanItemInts (see
 // kPrefillPlanHeaderInts), read with one scalar load.
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(4))) const i32x16 const_i32x16;
-
-__device__ inline PrefillWork plan_work(const int32_t* plan, int idx) {
-  const i32x16 d = ((const_i32x16*)(plan + kPrefillPlanHeaderInts))[idx];
-  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-  PrefillWork wk;
-  wk.s = d[0];
-  wk.t0 = d[1];
-  wk.q0 = d[2];
-  wk.q_len = d[3];
-  wk.kv = d[4];
-  wk.ntiles = d[5];
-  wk.full_tiles = d[6];
-  wk.npages = d[7];
-  wk.pg0 = w == 0 ? d[8] : w == 1 ? d[9] : w == 2 ? d[10] : d[11];
-  wk.pg1 = w == 0 ? d[12] : w == 1 ? d[13] : w == 2 ? d[14] : d[15];
-  return wk;
-}
 
 }  // namespace mva

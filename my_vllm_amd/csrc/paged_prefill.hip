@@ -174,10 +174,11 @@ int device_cu_count() {
 // chunks of 8 blocks (blocks are dealt to the 8 XCDs round-robin), then the
 // prefill workgroups.  The host sizes the decode part below the GPU's
 // resident capacity, so every decode wavefront starts at once and prefill
-// tiles fill the remaining slots (and the slots decode frees): HBM-bound
+// workgroups fill the remaining slots (and the slots decode frees): HBM-bound
 // decode streaming overlaps MFMA-bound prefill on the same CUs.  Prefill
-// blocks keep index % 8 == block % 8, so a prefill work item's KV head
-// (index % num_kv_heads) stays on the same XCD as in the prefill-only launch.
+// blocks keep index % 8 == block % 8, so prefill workgroup i, which serves
+// KV head i % num_kv_heads, runs on the XCD that serves that head in the
+// prefill-only launch.
 struct MixedRole {
   bool prefill;
   uint32_t index;  // prefill workgroup or decode workgroup number
@@ -190,8 +191,126 @@ __device__ inline MixedRole mixed_role(uint32_t block, uint32_t n_decode_wgs) {
   return {true, (c - cd) * 8u + r};
 }
 
-// Prefill workgroups run prefill tiles; decode workgroups run four decode
-// wavefronts each, with private LDS buffers.
+// Prefill sequences a MIXED launch orders in LDS.
+constexpr int kMixedPrefillSeqsMax = 1024;
+
+// The prefill workgroups of a MIXED launch are a persistent pool of
+// `per_head` workgroups per KV head.  Each builds the launch's query-tile
+// order in LDS from query_start_loc / seq_lens of the leading p.num_seqs
+// sequences -- sequences longest context first (ties by index), a
+// sequence's 128-row tiles largest key count first, as the PREFILL planner
+// orders them -- then takes tiles from its head's claim counter until none
+// are left.  So every tile run is a real tile, and no query count is needed
+// on the host.  A workgroup claims its next tile when its current one ends:
+// with about two tiles per workgroup, claiming one ahead would reserve
+// nearly every tile at the start and undo the balancing (measured 11%
+// slower on the prefill half of a budget-8192 batch).  A sequence with no queries, or more
+// queries than keys, has no tile.  The last workgroup of a head to leave
+// clears that head's counters for the next launch.
+template <typename T>
+__device__ void mixed_prefill_pool(const PrefillParams& p, int32_t* sched, uint32_t index, uint32_t per_head,
+                                   int* order, int* first_tile, int* claimed, lds_u8* k0, lds_u8* k1, lds_u8* v0,
+                                   lds_u8* v1) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int S = p.num_seqs;
+  const int BMT = p.tile_tokens;
+  const int h = (int)(index % (uint32_t)p.num_kv_heads);
+  int* const ctr = sched + kMixedPrefillCtrInt + h * kDecodeSchedLineInts;
+  if (tid == 0) *claimed = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // Tile order.  The K/V tile buffers are free until the first tile: k0
+  // holds the context lengths, k1 the tile counts by rank.
+  int* const kv_of = (int*)k0;
+  int* const tiles_of = (int*)k1;
+  for (int s = tid; s < S; s += 256) kv_of[s] = p.seq_lens[s];
+  __syncthreads();
+  for (int s = tid; s < S; s += 256) {
+    const int mine = kv_of[s];
+    int rank = 0;
+    for (int o = 0; o < S; ++o) {
+      const int v = kv_of[o];
+      rank += (v > mine) || (v == mine && o < s);
+    }
+    order[rank] = s;
+  }
+  __syncthreads();
+  for (int r = tid; r < S; r += 256) {
+    const int s = order[r];
+    const int q_len = p.query_start_loc[s + 1] - p.query_start_loc[s];
+    const int kv = kv_of[s];
+    tiles_of[r] = (q_len > 0 && kv >= q_len) ? (q_len + BMT - 1) / BMT : 0;
+  }
+  __syncthreads();
+  if (tid < 64) {
+    // Exclusive prefix sum over ranks, 64 at a time, by wave 0.
+    int carry = 0;
+    for (int c = 0; c < S; c += 64) {
+      const int v = c + lane < S ? tiles_of[c + lane] : 0;
+      int incl = v;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int up = __shfl_up(incl, off);
+        if (lane >= off) incl += up;
+      }
+      if (c + lane < S) first_tile[c + lane] = carry + incl - v;
+      carry += __shfl(incl, 63);
+    }
+    if (lane == 0) first_tile[S] = carry;
+  }
+  __syncthreads();
+  const int total = __builtin_amdgcn_readfirstlane(first_tile[S]);
+
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int idx = __builtin_amdgcn_readfirstlane(*claimed);
+  while (idx < total) {
+    // Rank of tile idx: the last rank whose first tile is <= idx.
+    int lo = 0, hi = S - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (first_tile[mid] <= idx) lo = mid;
+      else hi = mid - 1;
+    }
+    lo = __builtin_amdgcn_readfirstlane(lo);
+    PrefillWork wk;
+    wk.s = __builtin_amdgcn_readfirstlane(order[lo]);
+    wk.q0 = sload(p.query_start_loc, wk.s);
+    wk.q_len = sload(p.query_start_loc, wk.s + 1) - wk.q0;
+    wk.kv = sload(p.seq_lens, wk.s);
+    const int nt = (wk.q_len + BMT - 1) / BMT;
+    wk.t0 = (nt - 1 - (idx - __builtin_amdgcn_readfirstlane(first_tile[lo]))) * BMT;  // largest key count first
+    const int base_pos = wk.kv - wk.q_len;
+    const int kv_end = base_pos + min(wk.t0 + BMT, wk.q_len);  // keys [0, kv_end) are needed
+    wk.ntiles = (kv_end + kPrefillKeys - 1) / kPrefillKeys;
+    wk.full_tiles = min((base_pos + wk.t0 + 1) / kPrefillKeys, wk.ntiles);
+    wk.npages = (kv_end + kPageSize - 1) / kPageSize;
+    const int32_t* bt = p.block_tables + (int64_t)wk.s * p.bt_stride;
+    auto page = [&](int i) {
+      const int pg = sload(bt, min(i, wk.npages - 1));
+      return (pg >= 0 && pg < p.num_pages) ? pg : 0;
+    };
+    wk.pg0 = page(w);
+    wk.pg1 = page(kPrefillKeys / kPageSize + w);
+    prefill_core<T>(p, wk, h, k0, k1, v0, v1);
+    __syncthreads();  // every wave is done with this tile's LDS before `claimed` changes
+    if (tid == 0) *claimed = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    idx = __builtin_amdgcn_readfirstlane(*claimed);
+  }
+  if (tid == 0) {
+    // Every claim of this workgroup has returned (the last one ended the
+    // loop), so all claims on the counter precede the clear.
+    const int gone =
+        __hip_atomic_fetch_add(ctr + kMixedPrefillExitOffset, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (gone == (int)per_head - 1) {
+      __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(ctr + kMixedPrefillExitOffset, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// Prefill workgroups run the prefill pool; decode workgroups run four
+// decode wavefronts each, with private LDS buffers.
 template <typename T>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void paged_mixed_kernel(
     PrefillParams pp, DecodeParams dp, uint32_t n_prefill_wgs, uint32_t n_decode_wgs) {
@@ -199,13 +318,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   __shared__ __attribute__((aligned(16))) uint8_t k1[kPrefillTileBytes];
   __shared__ __attribute__((aligned(16))) uint8_t v0[kPrefillTileBytes];
   __shared__ __attribute__((aligned(16))) uint8_t v1[kPrefillTileBytes];
+  __shared__ int order[kMixedPrefillSeqsMax];
+  __shared__ int first_tile[kMixedPrefillSeqsMax + 1];
+  __shared__ int claimed;
   const MixedRole role = mixed_role(blockIdx.x, n_decode_wgs);
   if (role.prefill) {
     if (role.index >= n_prefill_wgs) return;
-    const int h = (int)(role.index % (uint32_t)pp.num_kv_heads);
-    const int item = (int)(role.index / (uint32_t)pp.num_kv_heads);
-    prefill_item<T>(pp, pp.items + (int64_t)item * kPrefillItemInts, h, (lds_u8*)k0, (lds_u8*)k1,
-                    (lds_u8*)v0, (lds_u8*)v1);
+    mixed_prefill_pool<T>(pp, dp.sched, role.index, n_prefill_wgs / (uint32_t)pp.num_kv_heads, order, first_tile,
+                          &claimed, (lds_u8*)k0, (lds_u8*)k1, (lds_u8*)v0, (lds_u8*)v1);
     return;
   }
   const int w = threadIdx.x >> 6;
@@ -216,6 +336,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   decode_wave<T>(dp, (int)wave, mine);
 }
 
+static_assert(kMixedPrefillSeqsMax * 4 <= kPrefillTileBytes, "context lengths fit one K/V tile buffer");
 static_assert(kDecodeWaveLdsBytes <= kPrefillTileBytes, "a decode wave's buffers must fit one prefill buffer");
 
 }  // namespace
@@ -223,8 +344,8 @@ static_assert(kDecodeWaveLdsBytes <= kPrefillTileBytes, "a decode wave's buffers
 int fill_prefill_params(PrefillParams& p, const void* q, int64_t q_token_stride, int64_t q_head_stride,
                         const void* k_cache, const void* v_cache, int64_t num_pages, int64_t page_stride,
                         int64_t token_stride, const int32_t* block_tables, int64_t block_table_stride,
-                        const int32_t* seq_lens, const int32_t* query_start_loc, const int32_t* items,
-                        int64_t num_items, void* out, int64_t out_token_stride, int64_t out_head_stride,
+                        const int32_t* seq_lens, const int32_t* query_start_loc, int64_t num_seqs,
+                        void* out, int64_t out_token_stride, int64_t out_head_stride,
                         int num_q_heads, int num_kv_heads, int head_dim, int page_size, float softmax_scale) {
   if (head_dim != kHeadDim) return set_error("paged attention: head_dim must be 128");
   if (page_size != kPageSize) return set_error("paged attention: page_size must be 16");
@@ -232,7 +353,7 @@ int fill_prefill_params(PrefillParams& p, const void* q, int64_t q_token_stride,
     return set_error("paged attention: num_q_heads must be a positive multiple of num_kv_heads");
   const int group = num_q_heads / num_kv_heads;
   if (group > 16) return set_error("paged attention: at most 16 query heads per KV head");
-  if (num_items < 0 || num_items * num_kv_heads > 0x7fffffffLL) return set_error("paged attention: invalid item count");
+  if (num_seqs < 0 || num_seqs > 0x7fffffffLL) return set_error("paged attention: invalid sequence count");
   if (num_pages <= 0) return set_error("paged attention: empty KV cache");
   const uint64_t align_bits = (uint64_t)(uintptr_t)q | (uint64_t)(uintptr_t)k_cache |
                               (uint64_t)(uintptr_t)v_cache | (uint64_t)(q_token_stride * 2) |
@@ -253,8 +374,7 @@ int fill_prefill_params(PrefillParams& p, const void* q, int64_t q_token_stride,
   p.bt_stride = block_table_stride;
   p.seq_lens = seq_lens;
   p.query_start_loc = query_start_loc;
-  p.items = items;
-  p.num_items = (int)num_items;
+  p.num_seqs = (int)num_seqs;
   p.out = out;
   p.out_tok_stride = out_token_stride;
   p.out_head_stride = out_head_stride;
@@ -289,11 +409,10 @@ extern "C" int mva_paged_prefill(const void* q, int64_t q_token_stride, int64_t 
   PrefillParams p;
   int rc = fill_prefill_params(p, q, q_token_stride, q_head_stride, k_cache, v_cache, num_pages, page_stride,
                                token_stride, block_tables, block_table_stride, seq_lens, query_start_loc,
-                               nullptr, 0, out, out_token_stride, out_head_stride, num_q_heads,
+                               num_seqs, out, out_token_stride, out_head_stride, num_q_heads,
                                num_kv_heads, head_dim, page_size, softmax_scale);
   if (rc) return rc;
   if (dtype != kBF16 && dtype != kF16) return set_error("paged attention: dtype must be bf16 or fp16");
-  if (num_seqs < 0 || num_seqs > 0x7fffffffLL) return set_error("paged attention: invalid sequence count");
   const int64_t need = mva_prefill_workspace_bytes(max_tiles);
   if (need < 0) return set_error("paged attention: invalid tile capacity");
   if (num_seqs == 0 || max_tiles == 0) return 0;
@@ -325,9 +444,8 @@ extern "C" int mva_paged_mixed(const void* q, int64_t q_token_stride, int64_t q_
                                const void* k_cache, const void* v_cache, int64_t num_pages,
                                int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
                                int64_t block_table_stride, const int32_t* seq_lens,
-                               const int32_t* query_start_loc, const int32_t* prefill_items,
-                               int64_t num_prefill_items, const int32_t* decode_items,
-                               int64_t num_decode_items, int64_t num_decode_waves,
+                               const int32_t* query_start_loc, int64_t num_prefill_seqs, int64_t max_prefill_tiles,
+                               const int32_t* decode_items, int64_t num_decode_items, int64_t num_decode_waves,
                                const int32_t* decode_merges, int64_t num_decode_merges, int64_t num_part_slots,
                                void* out, int64_t out_token_stride, int64_t out_head_stride,
                                void* workspace, int64_t workspace_bytes, int num_q_heads,
@@ -337,9 +455,13 @@ extern "C" int mva_paged_mixed(const void* q, int64_t q_token_stride, int64_t q_
   PrefillParams pp;
   int rc = fill_prefill_params(pp, q, q_token_stride, q_head_stride, k_cache, v_cache, num_pages, page_stride,
                                token_stride, block_tables, block_table_stride, seq_lens, query_start_loc,
-                               prefill_items, num_prefill_items, out, out_token_stride, out_head_stride,
+                               num_prefill_seqs, out, out_token_stride, out_head_stride,
                                num_q_heads, num_kv_heads, head_dim, page_size, softmax_scale);
   if (rc) return rc;
+  if (num_prefill_seqs > kMixedPrefillSeqsMax)
+    return set_error("paged attention: a MIXED launch takes at most 1024 prefill sequences");
+  if (max_prefill_tiles < 0 || max_prefill_tiles > 0x7fffffffLL)
+    return set_error("paged attention: invalid prefill tile capacity");
   DecodeParams dp;
   rc = fill_decode_params(dp, q, q_token_stride, q_head_stride, k_cache, v_cache, num_pages, page_stride,
                           token_stride, block_tables, block_table_stride, seq_lens, decode_items,
@@ -349,7 +471,16 @@ extern "C" int mva_paged_mixed(const void* q, int64_t q_token_stride, int64_t q_
                           workspace, workspace_bytes, num_q_heads, num_kv_heads, head_dim, page_size,
                           softmax_scale);
   if (rc) return rc;
-  const int64_t n_prefill_wgs = num_prefill_items * num_kv_heads;
+  // Prefill pool: two workgroups per CU (the CU's eight wave slots), a whole
+  // number per KV head, never more than the tiles can use.
+  int64_t per_head = 0;
+  if (num_prefill_seqs > 0 && max_prefill_tiles > 0) {
+    if (num_kv_heads > kMixedPrefillMaxHeads) return set_error("paged attention: a MIXED launch takes at most 64 KV heads");
+    if (workspace == nullptr) return set_error("paged attention: MIXED launches need the decode workspace");
+    per_head = 2 * (int64_t)device_cu_count() / num_kv_heads;
+    per_head = per_head < 1 ? 1 : (per_head > max_prefill_tiles ? max_prefill_tiles : per_head);
+  }
+  const int64_t n_prefill_wgs = per_head * num_kv_heads;
   const int64_t n_decode_wgs = num_decode_items > 0 ? (num_decode_waves + 3) / 4 : 0;
   if (n_prefill_wgs + n_decode_wgs > 0x7fffff00LL) return set_error("paged attention: too many work items");
   if (n_prefill_wgs + n_decode_wgs == 0) return 0;

@@ -22,8 +22,6 @@ PREFILL_ROWS = 128
 # Query rows per tile of mva_paged_prefill's kernel (the MIXED kernel's
 # prefill tiles have PREFILL_ROWS).
 PREFILL_STREAM_ROWS = 256
-# int32 fields per prefill work item of the MIXED launch (kPrefillItemInts).
-PREFILL_ITEM_INTS = 4
 # Device-built prefill tile list: header ints (tile count + per-head claim
 # counters) and ints per tile record (kPrefillPlanHeaderInts / ItemInts).
 PREFILL_PLAN_HEADER_INTS = 32 * 128
@@ -543,6 +541,19 @@ def prefill_max_tiles(num_prefill_tokens: int, num_prefill_seqs: int, num_q_head
     return num_prefill_tokens // tile + num_prefill_seqs
 
 
+def mixed_prefill_max_tiles(num_prefill_tokens: int, num_prefill_seqs: int, num_q_heads: int,
+                            num_kv_heads: int) -> int:
+    """Bound on the 128-row query tiles of a MIXED launch's prefill part."""
+    tile = PREFILL_ROWS // (num_q_heads // num_kv_heads)
+    return num_prefill_tokens // tile + num_prefill_seqs
+
+
+# Prefill sequences and KV heads one MIXED launch takes (kMixedPrefillSeqsMax,
+# kMixedPrefillMaxHeads); larger MIXED batches run as prefill + decode.
+MIXED_PREFILL_SEQS_MAX = 1024
+MIXED_MAX_KV_HEADS = 64
+
+
 def prefill_workspace_bytes(max_tiles: int) -> int:
     nbytes = int(_native.query("mva_prefill_workspace_bytes", max_tiles))
     if nbytes < 0:
@@ -587,8 +598,8 @@ def paged_mixed(
     block_tables: torch.Tensor,
     seq_lens: torch.Tensor,
     query_start_loc: torch.Tensor,
-    prefill_items: torch.Tensor,
-    num_prefill_items: int,
+    num_prefill_seqs: int,
+    max_prefill_tiles: int,
     decode_items: torch.Tensor | None,
     num_decode_items: int,
     num_decode_waves: int,
@@ -596,20 +607,22 @@ def paged_mixed(
     num_decode_merges: int,
     num_part_slots: int,
     out: torch.Tensor,
-    workspace: torch.Tensor | None,
+    workspace: torch.Tensor,
     softmax_scale: float,
 ) -> None:
-    """One launch: prefill tiles write ``out[:P]``, decode pieces write ``out[P:]``."""
-    ws_ptr = workspace.data_ptr() if workspace is not None else 0
-    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    """One launch: prefill tiles write ``out[:P]``, decode pieces write ``out[P:]``.
+
+    The prefill tiles of the leading ``num_prefill_seqs`` sequences are
+    derived on the device; ``max_prefill_tiles`` bounds them (see
+    :func:`mixed_prefill_max_tiles`).  ``workspace`` is the decode workspace.
+    """
     _native.call(
         "mva_paged_mixed",
         *_paged_args(q, k_cache, v_cache, block_tables, seq_lens),
-        query_start_loc.data_ptr(),
-        prefill_items.data_ptr(), num_prefill_items,
+        query_start_loc.data_ptr(), int(num_prefill_seqs), int(max_prefill_tiles),
         decode_items.data_ptr() if decode_items is not None else 0, num_decode_items, num_decode_waves,
         decode_merges.data_ptr() if decode_merges is not None else 0, num_decode_merges, num_part_slots,
         out.data_ptr(), out.stride(0), out.stride(1),
-        ws_ptr, ws_bytes,
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(),
         *_tail_args(q, k_cache, softmax_scale),
     )

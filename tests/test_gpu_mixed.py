@@ -91,3 +91,46 @@ def test_reference_numeric_cases(gpu, mode, case):
     assert plan.route is route
     assert out.shape == batch.q.shape and out.dtype == torch.bfloat16
     assert_attention_close(out, expected(batch))
+
+
+def test_mixed_many_prefill_sequences_device_tiles(gpu):
+    # 150 prefill sequences: the single launch orders their tiles on the
+    # device across several 64-sequence scan chunks, sequences with equal
+    # contexts included; prefill rows match the split route bit for bit.
+    import numpy as np
+
+    rng = np.random.default_rng(17)
+    q = [int(x) for x in rng.integers(1, 40, size=150)]
+    kv = [n + int(rng.choice([0, 16, 37, 200])) for n in q]
+    q += [1] * 20
+    kv += [int(x) for x in rng.integers(1, 600, size=20)]
+    batch = make_paged_batch(97, q, kv, 150, 16, 4)
+    out_u, plan_u = run_backend(batch, gpu, mode="unified")
+    out_u = out_u.clone()
+    assert plan_u.route is AttentionRoute.MIXED_UNIFIED and plan_u.metadata.mixed_prefill_max_tiles > 0
+    out_s, _ = run_backend(batch, gpu, mode="split")
+    rows = sum(q[:150])
+    assert torch.equal(out_u[:rows], out_s[:rows])
+    assert_attention_close(out_u, expected(batch))
+
+
+def test_mixed_launch_leaves_its_counters_clear(gpu):
+    # The prefill pool's claim and exit counters (and the decode claims) are
+    # back at zero after every launch, so the next launch on the same
+    # workspace starts from tile 0.
+    from my_vllm_amd import ops
+    from my_vllm_amd.attention_backend import MI355XAttentionBackend
+    from tests.test_gpu_prefill import to_device
+
+    batch = make_paged_batch(101, [70, 300, 1, 1, 1], [70, 900, 40, 700, 2000], 2, 32, 8)
+    backend = MI355XAttentionBackend(32, 8, 128, 16, torch.bfloat16)
+    common, qd, kc, vc = to_device(batch, gpu)
+    plan = backend.build_plan(common)
+    empty = qd.new_empty((0, 8, 128))
+    first = backend.forward(qd, empty, empty, kc, vc, plan).clone()
+    again = backend.forward(qd, empty, empty, kc, vc, plan)
+    torch.cuda.synchronize()
+    assert torch.equal(first, again)
+    sched = ops.decode_workspace_bytes(0, 1, 1)
+    assert int(backend._workspace[:sched].view(torch.int32).abs().sum().item()) == 0
+    assert_attention_close(again, expected(batch))

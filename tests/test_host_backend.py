@@ -21,7 +21,6 @@ from my_vllm_amd.attention_backend import (
     integrate,
     make_decode_plan,
     make_decode_plan_listed,
-    make_prefill_items,
 )
 from my_vllm_amd.contract import AttentionBackend, AttentionPlan, AttentionRoute, BatchType, CommonAttentionMetadata
 from tests import _foreign_contract as foreign
@@ -117,7 +116,7 @@ def test_trusted_planning_reads_no_device_values(monkeypatch):
     plan = backend.build_plan(common)
     monkeypatch.undo()
     assert plan.route is AttentionRoute.MIXED_UNIFIED
-    assert plan.metadata.num_decode_items > 0 and plan.metadata.num_prefill_items > 0
+    assert plan.metadata.num_decode_items > 0 and plan.metadata.mixed_prefill_max_tiles > 0
 
 
 def test_validation_errors_follow_the_reference():
@@ -375,25 +374,33 @@ def test_listed_decode_plan_edges():
 
 
 @pytest.mark.parametrize("seed", range(10))
-def test_prefill_items_cover_every_tile_once(seed):
+def test_prefill_tile_bounds_hold_for_any_split_of_the_tokens(seed):
+    # The host knows only the prefill token and sequence counts; the bounds
+    # must cover every split of those tokens into sequences (the device
+    # derives the real tiles, 256-row for PREFILL, 128-row for MIXED).
     rng = np.random.default_rng(100 + seed)
-    q_ub = rng.integers(1, 700, size=int(rng.integers(1, 12)))
-    kv_ub = q_ub + rng.integers(0, 900, size=q_ub.size)
-    tile = int(rng.choice([8, 16, 32, 64, 128]))
-    items = make_prefill_items(q_ub, kv_ub, tile)
-    assert items.dtype == np.int32 and items.shape[1] == ops.PREFILL_ITEM_INTS
-    got = sorted((int(s), int(t)) for s, t in items[:, :2])
-    want = sorted((s, t) for s in range(q_ub.size) for t in range(0, int(q_ub[s]), tile))
-    assert got == want
-    # Grouped by sequence, longest context first; inside a sequence the
-    # tiles with the most keys come first.
-    seqs = [int(s) for s in items[:, 0]]
-    groups = [s for i, s in enumerate(seqs) if i == 0 or s != seqs[i - 1]]
-    assert sorted(groups) == list(range(q_ub.size)), "each sequence's tiles are contiguous"
-    assert all(kv_ub[a] >= kv_ub[b] for a, b in zip(groups, groups[1:])), "longest context first"
-    cost = [int(kv_ub[s] - q_ub[s] + min(t + tile, q_ub[s])) for s, t in items[:, :2]]
-    assert all(a >= b for a, b, sa, sb in zip(cost, cost[1:], seqs, seqs[1:]) if sa == sb), \
-        "largest key count first within a sequence"
+    n = int(rng.integers(1, 40))
+    q = rng.integers(1, 3000, size=n)
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    hq = hkv * int(rng.choice([1, 2, 3, 4, 8, 16]))
+    g = hq // hkv
+    for rows, bound in ((ops.PREFILL_STREAM_ROWS, ops.prefill_max_tiles),
+                        (ops.PREFILL_ROWS, ops.mixed_prefill_max_tiles)):
+        tile = rows // g
+        assert int(np.sum(-(-q // tile))) <= bound(int(q.sum()), n, hq, hkv)
+
+
+def test_mixed_beyond_one_launch_limits_runs_as_two_launches():
+    # More prefill sequences than one MIXED launch takes: the unified
+    # backend plans the batch for prefill + decode launches.
+    backend = HostBackend(16, 4, 128, 16, torch.bfloat16)
+    n = ops.MIXED_PREFILL_SEQS_MAX + 1
+    common = _common((1,) * n + (1,), (5,) * n + (9,), n, trusted=True)
+    plan = backend.build_plan(common)
+    assert plan.route is AttentionRoute.MIXED_UNIFIED
+    assert plan.metadata.mixed_prefill_max_tiles == 0 and plan.metadata.prefill_max_tiles > 0
+    small = backend.build_plan(_common((5, 1), (21, 13), 1, trusted=True))
+    assert small.metadata.mixed_prefill_max_tiles > 0
 
 
 @pytest.mark.parametrize("seed", range(5))
