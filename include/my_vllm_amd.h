@@ -327,8 +327,11 @@ int mva_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_stri
  * persistent pool of prefill workgroups; max_prefill_tiles bounds their
  * number (num_prefill_tokens / tile_tokens + num_prefill_seqs) and only
  * sizes the pool.  The workspace (mva_decode_workspace_bytes) also holds the
- * pool's claim counters, which the launch leaves at zero.  At most 64 KV
- * heads when prefill sequences are present.
+ * pool's claim counters and the split-K arrival counters, which the launch
+ * leaves at zero.  Split decode segments are merged inside the launch: the
+ * last piece of a segment to finish combines the partials, so no merge list
+ * or merge kernel is involved.  At most 64 KV heads when prefill sequences
+ * are present.
  * Replaces FlashInfer BatchAttention.plan/run on the reference's MIXED_UNIFIED
  * route (nanovllm/layers/attention_backend.py:841-857, :998-1009).
  */
@@ -338,8 +341,7 @@ int mva_paged_mixed(const void* q, int64_t q_token_stride, int64_t q_head_stride
                     int64_t block_table_stride, const int32_t* seq_lens,
                     const int32_t* query_start_loc, int64_t num_prefill_seqs, int64_t max_prefill_tiles,
                     const int32_t* decode_items, int64_t num_decode_items, int64_t num_decode_waves,
-                    const int32_t* decode_merges, int64_t num_decode_merges, int64_t num_part_slots,
-                    void* out, int64_t out_token_stride, int64_t out_head_stride,
+                    int64_t num_part_slots, void* out, int64_t out_token_stride, int64_t out_head_stride,
                     void* workspace, int64_t workspace_bytes, int num_q_heads, int num_kv_heads,
                     int head_dim, int page_size, float softmax_scale, int dtype, void* stream);
 

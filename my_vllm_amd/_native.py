@@ -134,7 +134,7 @@ _SIGNATURES = {
             _c_void_p, _c_void_p, _i64, _i64, _i64,
             _c_void_p, _i64, _c_void_p, _c_void_p,
             _i64, _i64, _c_void_p, _i64, _i64,  # prefill seqs, max prefill tiles, decode items, waves
-            _c_void_p, _i64, _i64,  # decode merges, num merges, num_part_slots
+            _i64,  # num_part_slots
             _c_void_p, _i64, _i64,
             _c_void_p, _i64,
             _i32, _i32, _i32, _i32, _f32, _i32, _c_void_p,

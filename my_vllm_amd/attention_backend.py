@@ -568,7 +568,8 @@ class MI355XAttentionBackendMixin:
                     self.num_kv_heads,
                     waves,
                 )
-            merges = ops.decode_merge_list(items)
+            # The single MIXED launch merges split segments itself.
+            merges = np.zeros((0, ops.DECODE_ITEM_INTS), np.int32) if one_launch else ops.decode_merge_list(items)
             num_decode_items = items.shape[0]
             num_decode_merges = merges.shape[0]
             # Pieces, merge entries and piece-list offsets share one
@@ -1031,8 +1032,6 @@ class MI355XAttentionBackendMixin:
             metadata.decode_items,
             metadata.num_decode_items,
             metadata.num_decode_waves,
-            metadata.decode_merges,
-            metadata.num_decode_merges,
             metadata.num_decode_part_slots,
             output,
             workspace,

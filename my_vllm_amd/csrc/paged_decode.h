@@ -110,6 +110,10 @@ struct DecodeParams {
   int64_t out_head_stride;
   float* part_lse;    // [slots][Hkv][G]
   float* part_o;      // [slots][Hkv][G][D]
+  // Split-K merges inside the launch (MIXED), or nullptr for the merge
+  // kernel: the arrival counter of segment (part_base, KV head) at
+  // arrive[part_base * Hkv + kv_head]; the last piece to arrive merges.
+  int32_t* arrive;
   int num_kv_heads;
   int group;  // query heads per KV head, 1..16
   float scale_log2;
@@ -289,6 +293,9 @@ constexpr int kMixedPrefillExitOffset = 16;
 static_assert((kMixedPrefillCtrInt + kMixedPrefillMaxHeads * kDecodeSchedLineInts) * 4 <= kDecodeSchedBytes,
               "MIXED prefill counters");
 
+template <typename T, bool kAgent>
+__device__ void merge_segment(const DecodeParams& p, const i32x8& d, int g);
+
 // One wavefront of a decode launch (`wave` in [0, num_waves)); `lds` is its
 // kDecodeWaveLdsBytes of LDS.
 //
@@ -315,7 +322,7 @@ static_assert((kMixedPrefillCtrInt + kMixedPrefillMaxHeads * kDecodeSchedLineInt
 // two KV heads.  The older of the two wins issue arbitration and would finish
 // first; each wavefront publishes its page count and keeps priority 2 unless
 // it is ahead of its partner, so the pair stays level.
-template <typename T>
+template <typename T, bool kMergeInLaunch = false>
 __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds, int* progress = nullptr) {
   typedef typename Elem<T>::v8 V8;
   typedef typename Elem<T>::v4 V4;
@@ -356,6 +363,7 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds, int* p
 
   // ---- piece state --------------------------------------------------------
   i32x8 X = desc_at(wave);
+  int xi = wave;  // X's index in the piece array
   // Piece lists: nx is the next unassigned entry of this wavefront's range
   // [nx, nx_end).
   const bool listed = p.wave_extra != nullptr;
@@ -487,6 +495,30 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds, int* p
     }
   };
 
+  // In-launch merges (kMergeInLaunch, p.arrive): the split pieces this wavefront finished
+  // wait in the lanes of split_list (piece indices) until it leaves.  It
+  // then waits for its partial stores (written through to memory), counts
+  // each piece in at its segment's arrival counter, and the piece that
+  // arrives last merges the segment with agent-scope loads and clears the
+  // counter.  Arrivals at exit keep atomics out of the page stream; a
+  // 65th split piece flushes the list first.
+  int split_list = 0;
+  int nsplit = 0;
+  auto settle = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    for (int j = 0; j < nsplit; ++j) {
+      const i32x8 d = desc_at(__builtin_amdgcn_readlane(split_list, j));
+      int* const ctr = p.arrive + (int64_t)d[5] * Hkv + d[7];
+      int old = 0;
+      if (lane == 0) old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__builtin_amdgcn_readfirstlane(old) == d[4] - 1) {
+        for (int g = 0; g < G; ++g) merge_segment<T, true>(p, d, g);
+        if (lane == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    nsplit = 0;
+  };
+
   // End of piece X: the final output, or its split-K partial (normalised o
   // and log2-sum-exp, device-scope stores that go past this XCD's L2).
   auto finish_piece = [&]() __attribute__((always_inline)) {
@@ -513,6 +545,11 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds, int* p
       for (int mt = 0; mt < 8; ++mt) store16_device_untracked(po + 16 * mt, __builtin_bit_cast(u32x4, o[mt] * inv));
       if (q4 == 0)
         store4_device_untracked(&p.part_lse[slot * G + c], l_tot > 0.f ? m + fast_log2(l_tot) : -INFINITY);
+    }
+    if constexpr (kMergeInLaunch) {
+      if (nsplit == 64) settle();
+      split_list = lane == nsplit ? xi : split_list;
+      ++nsplit;
     }
   };
 
@@ -655,6 +692,7 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds, int* p
     finish_piece();
     if (yi >= N) break;
     X = Y;
+    xi = yi;
     seq_len = y_len;
     bt_lo = io.bt_lo;
     bt_hi = io.bt_hi;
@@ -670,6 +708,10 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds, int* p
     m = -INFINITY;
     l = 0.f;
     i = 0;
+  }
+
+  if constexpr (kMergeInLaunch) {
+    if (nsplit > 0) settle();
   }
 
   // Count this wavefront out; the last one resets the scheduler for the next
@@ -690,23 +732,34 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds, int* p
   }
 }
 
-// Split-K merge of one (split segment, query head g): the wavefront's index
-// v selects merge entry v / G (a piece descriptor {seq, -, -, -, n_chunks,
-// part_base, q_row, kv_head} of a segment cut into n_chunks > 1 pieces) and
-// g = v % G, and writes
+// Partial rows and log-sum-exps, read normally (after the launch that wrote
+// them) or with agent-scope loads (inside it: the lines come from memory,
+// where the writers' stores went through their own XCD's L2).
+template <bool kAgent>
+__device__ inline float part_load(const float* a) {
+  if constexpr (kAgent) return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else return *a;
+}
+template <bool kAgent>
+__device__ inline f32x2 part_load2(const float* a) {
+  if constexpr (kAgent) return f32x2{part_load<true>(a), part_load<true>(a + 1)};
+  else return *reinterpret_cast<const f32x2*>(a);
+}
+
+// Split-K merge of one (split segment, query head g): d is a piece
+// descriptor {seq, -, -, -, n_chunks, part_base, q_row, kv_head} of a
+// segment cut into n_chunks > 1 pieces; writes
 //   o = sum_k w_k o_k / sum_k w_k,  w_k = 2^(lse_k - max_k lse_k)
 // over the segment's chunks k.  Lane L owns chunks L, L+64, ... of the
 // log-sum-exp pass and output columns d = 2L, 2L+1 of the weighted sum.
-// Runs in the kernel after the decode kernel, which makes every partial
-// visible.
-template <typename T>
-__device__ void decode_merge_wave(const DecodeParams& p, const int32_t* __restrict__ merges, int64_t v) {
+// Runs in the kernel after the decode kernel (kAgent false: the kernel
+// boundary makes every partial visible) or inside the launch after the
+// segment's last arrival (kAgent true).
+template <typename T, bool kAgent>
+__device__ void merge_segment(const DecodeParams& p, const i32x8& d, int g) {
   const int lane = threadIdx.x & 63;
   const int G = p.group;
   const int Hkv = p.num_kv_heads;
-  // v is wave-uniform: the descriptor comes in through scalar loads.
-  const i32x8 d = ((const_i32x8*)merges)[v / G];
-  const int g = (int)(v % G);
   const int n = d[4];
   const int pbase = d[5];
   const int64_t qrow = d[6];
@@ -720,17 +773,17 @@ __device__ void decode_merge_wave(const DecodeParams& p, const int32_t* __restri
   f32x2 rows[kBatch];
 #pragma unroll
   for (int j = 0; j < kBatch; ++j)
-    rows[j] = *reinterpret_cast<const f32x2*>(p.part_o + slot(min(j, n - 1)) * kHeadDim + 2 * lane);
-  float lse0 = lane < n ? p.part_lse[slot(lane)] : -INFINITY;  // chunks 0..63, kept for the weights
+    rows[j] = part_load2<kAgent>(p.part_o + slot(min(j, n - 1)) * kHeadDim + 2 * lane);
+  float lse0 = lane < n ? part_load<kAgent>(&p.part_lse[slot(lane)]) : -INFINITY;  // chunks 0..63, kept for the weights
   float mx = lse0;
   for (int k0 = 64; k0 < n; k0 += 64)
-    if (k0 + lane < n) mx = fmaxf(mx, p.part_lse[slot(k0 + lane)]);
+    if (k0 + lane < n) mx = fmaxf(mx, part_load<kAgent>(&p.part_lse[slot(k0 + lane)]));
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
   float a0 = 0.f, a1 = 0.f, wsum = 0.f;
   for (int k0 = 0; k0 < n; k0 += 64) {
     const int k = k0 + lane;
-    const float lse = k0 == 0 ? lse0 : (k < n ? p.part_lse[slot(k)] : -INFINITY);
+    const float lse = k0 == 0 ? lse0 : (k < n ? part_load<kAgent>(&p.part_lse[slot(k)]) : -INFINITY);
     const float w = (k < n && mx != -INFINITY) ? fast_exp2(lse - mx) : 0.f;
     wsum += w;
     const int cnt = min(64, n - k0);
@@ -738,7 +791,7 @@ __device__ void decode_merge_wave(const DecodeParams& p, const int32_t* __restri
       if (k0 + j0 > 0) {
 #pragma unroll
         for (int j = 0; j < kBatch; ++j)
-          rows[j] = *reinterpret_cast<const f32x2*>(p.part_o + slot(min(k0 + j0 + j, n - 1)) * kHeadDim + 2 * lane);
+          rows[j] = part_load2<kAgent>(p.part_o + slot(min(k0 + j0 + j, n - 1)) * kHeadDim + 2 * lane);
       }
 #pragma unroll
       for (int j = 0; j < kBatch; ++j) {
@@ -758,6 +811,15 @@ __device__ void decode_merge_wave(const DecodeParams& p, const int32_t* __restri
   T* op = (T*)p.out + qrow * p.out_tok_stride + (int64_t)(h * G + g) * p.out_head_stride + 2 * lane;
   op[0] = (T)(a0 * winv);
   op[1] = (T)(a1 * winv);
+}
+
+// Split-K merge of one (split segment, query head g) of the merge list:
+// wavefront v takes merge entry v / G and g = v % G.
+template <typename T>
+__device__ void decode_merge_wave(const DecodeParams& p, const int32_t* __restrict__ merges, int64_t v) {
+  // v is wave-uniform: the descriptor comes in through scalar loads.
+  const i32x8 d = ((const_i32x8*)merges)[v / p.group];
+  merge_segment<T, false>(p, d, (int)(v % p.group));
 }
 
 }  // namespace mva

@@ -17,6 +17,7 @@ int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, i
                        float softmax_scale);
 int launch_decode_merge(const DecodeParams& p, const int32_t* merges, int64_t num_merges, int dtype,
                         hipStream_t stream);
+int32_t* decode_arrival_counters(void* workspace, int64_t slots, int hkv, int group);
 
 namespace {
 
@@ -333,7 +334,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   if (wave >= dp.num_waves) return;
   // Each decode wavefront gets one of the four prefill buffers.
   lds_u8* mine = (lds_u8*)(w == 0 ? k0 : w == 1 ? k1 : w == 2 ? v0 : v1);
-  decode_wave<T>(dp, (int)wave, mine);
+  decode_wave<T, true>(dp, (int)wave, mine);
 }
 
 static_assert(kMixedPrefillSeqsMax * 4 <= kPrefillTileBytes, "context lengths fit one K/V tile buffer");
@@ -446,8 +447,7 @@ extern "C" int mva_paged_mixed(const void* q, int64_t q_token_stride, int64_t q_
                                int64_t block_table_stride, const int32_t* seq_lens,
                                const int32_t* query_start_loc, int64_t num_prefill_seqs, int64_t max_prefill_tiles,
                                const int32_t* decode_items, int64_t num_decode_items, int64_t num_decode_waves,
-                               const int32_t* decode_merges, int64_t num_decode_merges, int64_t num_part_slots,
-                               void* out, int64_t out_token_stride, int64_t out_head_stride,
+                               int64_t num_part_slots, void* out, int64_t out_token_stride, int64_t out_head_stride,
                                void* workspace, int64_t workspace_bytes, int num_q_heads,
                                int num_kv_heads, int head_dim, int page_size, float softmax_scale,
                                int dtype, void* stream) {
@@ -465,12 +465,13 @@ extern "C" int mva_paged_mixed(const void* q, int64_t q_token_stride, int64_t q_
   DecodeParams dp;
   rc = fill_decode_params(dp, q, q_token_stride, q_head_stride, k_cache, v_cache, num_pages, page_stride,
                           token_stride, block_tables, block_table_stride, seq_lens, decode_items,
-                          num_decode_items, num_decode_waves, nullptr, decode_merges, num_decode_merges, num_part_slots,
-                          out,
+                          num_decode_items, num_decode_waves, nullptr, nullptr, 0, num_part_slots, out,
                           out_token_stride, out_head_stride,
                           workspace, workspace_bytes, num_q_heads, num_kv_heads, head_dim, page_size,
                           softmax_scale);
   if (rc) return rc;
+  // Split-K segments are merged inside the launch by their last piece.
+  dp.arrive = decode_arrival_counters(workspace, num_part_slots, num_kv_heads, dp.group);
   // Prefill pool: two workgroups per CU (the CU's eight wave slots), a whole
   // number per KV head, never more than the tiles can use.
   int64_t per_head = 0;
@@ -492,7 +493,5 @@ extern "C" int mva_paged_mixed(const void* q, int64_t q_token_stride, int64_t q_
   else if (dtype == kF16)
     hipLaunchKernelGGL(paged_mixed_kernel<_Float16>, grid, dim3(256), 0, s, pp, dp, np, nd);
   else return set_error("paged attention: dtype must be bf16 or fp16");
-  rc = check_launch("paged_mixed");
-  if (rc) return rc;
-  return launch_decode_merge(dp, decode_merges, num_decode_merges, dtype, s);
+  return check_launch("paged_mixed");
 }

@@ -603,8 +603,6 @@ def paged_mixed(
     decode_items: torch.Tensor | None,
     num_decode_items: int,
     num_decode_waves: int,
-    decode_merges: torch.Tensor | None,
-    num_decode_merges: int,
     num_part_slots: int,
     out: torch.Tensor,
     workspace: torch.Tensor,
@@ -614,14 +612,16 @@ def paged_mixed(
 
     The prefill tiles of the leading ``num_prefill_seqs`` sequences are
     derived on the device; ``max_prefill_tiles`` bounds them (see
-    :func:`mixed_prefill_max_tiles`).  ``workspace`` is the decode workspace.
+    :func:`mixed_prefill_max_tiles`).  Split decode segments are merged
+    inside the launch (no merge list).  ``workspace`` is the decode
+    workspace.
     """
     _native.call(
         "mva_paged_mixed",
         *_paged_args(q, k_cache, v_cache, block_tables, seq_lens),
         query_start_loc.data_ptr(), int(num_prefill_seqs), int(max_prefill_tiles),
         decode_items.data_ptr() if decode_items is not None else 0, num_decode_items, num_decode_waves,
-        decode_merges.data_ptr() if decode_merges is not None else 0, num_decode_merges, num_part_slots,
+        num_part_slots,
         out.data_ptr(), out.stride(0), out.stride(1),
         workspace.data_ptr(), workspace.numel() * workspace.element_size(),
         *_tail_args(q, k_cache, softmax_scale),

@@ -134,3 +134,17 @@ def test_mixed_launch_leaves_its_counters_clear(gpu):
     sched = ops.decode_workspace_bytes(0, 1, 1)
     assert int(backend._workspace[:sched].view(torch.int32).abs().sum().item()) == 0
     assert_attention_close(again, expected(batch))
+
+
+def test_mixed_in_launch_merges_flush_a_long_list(gpu, monkeypatch):
+    # One decode wavefront runs 640 split pieces (40 sequences x 8 KV heads x
+    # 2 chunks): its list of pieces awaiting arrival fills (64 entries) and
+    # is flushed ten times; every segment is still merged exactly once.
+    monkeypatch.setenv("MVA_DECODE_WAVES", "1")
+    q = [40] + [1] * 40
+    kv = [300] + [2080] * 40
+    batch = make_paged_batch(103, q, kv, 1, 16, 8)
+    out, plan = run_backend(batch, gpu)
+    assert plan.route is AttentionRoute.MIXED_UNIFIED
+    assert plan.metadata.num_decode_items == 640 and plan.metadata.num_decode_merges == 0
+    assert_attention_close(out, expected(batch))
