@@ -293,7 +293,9 @@ def extra_measurements(device, steps: int):
         kc, vc = batch.k_cache.to(device), batch.v_cache.to(device)
         plan = backend.build_plan(common)
         empty = q.new_empty((0, hkv, 128))
-        return time_launches(lambda i: backend.forward(q, empty, empty, kc, vc, plan), iters, 3)
+        # Median of 5 timed regions, as for the headline: one region of 20
+        # MFMA-bound launches swings with the clock by 10% or more.
+        return time_launches(lambda i: backend.forward(q, empty, empty, kc, vc, plan), iters, 3, repeats=5)
 
     # PURE_PREFILL with prefix, Qwen3-8B.
     # The same CPU-seeded draw the parity tests check.
