@@ -148,3 +148,17 @@ def test_mixed_in_launch_merges_flush_a_long_list(gpu, monkeypatch):
     assert plan.route is AttentionRoute.MIXED_UNIFIED
     assert plan.metadata.num_decode_items == 640 and plan.metadata.num_decode_merges == 0
     assert_attention_close(out, expected(batch))
+
+
+def test_mixed_beyond_one_launch_runs_prefill_then_decode(gpu):
+    # More prefill sequences than one MIXED launch orders (1024): the unified
+    # backend runs the batch as prefill + decode launches, with the same rows.
+    from my_vllm_amd import ops
+
+    n = ops.MIXED_PREFILL_SEQS_MAX + 3
+    q = [2] * n + [1, 1]
+    kv = [9] * n + [300, 40]
+    batch = make_paged_batch(107, q, kv, n, 16, 8)
+    out, plan = run_backend(batch, gpu)
+    assert plan.route is AttentionRoute.MIXED_UNIFIED and plan.metadata.mixed_prefill_max_tiles == 0
+    assert_attention_close(out, expected(batch))

@@ -229,3 +229,23 @@ def test_device_tile_plan_is_exact(gpu, hq, hkv):
     bt = batch.common.block_tables
     want = [r[:8] + [int(bt[r[0], i]) for i in r[8:]] for r in want]
     assert got == want
+
+
+def test_more_sequences_than_the_planner_sorts(gpu):
+    # 2100 short prefill sequences, more than the planner sorts (2048): the
+    # device plans them in batch order, in two rounds; every row is still
+    # computed once.
+    import numpy as np
+
+    rng = np.random.default_rng(23)
+    n = 2100
+    q = [int(x) for x in rng.integers(1, 6, size=n)]
+    kv = [x + int(rng.integers(0, 40)) for x in q]
+    batch = make_paged_batch(137, q, kv, n, 8, 8)
+    out, plan = run_backend(batch, gpu)
+    assert plan.route is AttentionRoute.PREFILL
+    seqs = [0, 1, 1000, 2047, 2048, 2049, n - 1]
+    exp, rows = expected(batch, seqs)
+    assert_attention_close(out.cpu()[rows], exp)
+    # Rows of every sequence are written (no NaN from the backend's buffer).
+    assert bool(torch.isfinite(out.float()).all())
