@@ -309,6 +309,44 @@ def _to_device(array: np.ndarray, device: torch.device) -> torch.Tensor:
     return host.pin_memory().to(device, non_blocking=True)
 
 
+class PinnedStaging:
+    """A ring of pinned host buffers for the per-step int32 work lists.
+
+    Each host-to-device copy takes the next buffer of the ring, allocated
+    once and grown only when a list outgrows it; before refilling a buffer
+    the host waits on the event of that buffer's previous copy, issued
+    ``slots`` copies earlier and normally long complete.  So planning pins
+    no memory per step and the host can run ahead of the device by up to
+    ``slots`` steps.
+    """
+
+    def __init__(self, slots: int = 4):
+        self._buffers: list[torch.Tensor | None] = [None] * slots
+        self._events: list[Any] = [None] * slots
+        self._next = 0
+
+    def to_device(self, array: np.ndarray, device: torch.device) -> torch.Tensor:
+        host = np.ascontiguousarray(array, dtype=np.int32).reshape(-1)
+        if device.type != "cuda":
+            return torch.from_numpy(host.copy()).to(device)
+        k = self._next
+        self._next = (k + 1) % len(self._buffers)
+        if self._events[k] is not None:
+            self._events[k].synchronize()
+        buf = self._buffers[k]
+        if buf is None or buf.numel() < host.size:
+            buf = torch.empty(max(host.size, 4096, 2 * (buf.numel() if buf is not None else 0)),
+                              dtype=torch.int32, pin_memory=True)
+            self._buffers[k] = buf
+        buf[: host.size].copy_(torch.from_numpy(host))
+        out = torch.empty(host.size, dtype=torch.int32, device=device)
+        out.copy_(buf[: host.size], non_blocking=True)
+        event = torch.cuda.Event()
+        event.record()
+        self._events[k] = event
+        return out
+
+
 def _device_arch(device: torch.device) -> str:
     props = torch.cuda.get_device_properties(device)
     return getattr(props, "gcnArchName", "") or ""
@@ -336,11 +374,14 @@ class MI355XFullDecodeGraphState:
     block_tables_buffer: torch.Tensor
     seq_lens_buffer: torch.Tensor
     plan_buffer: torch.Tensor
-    plan_staging: torch.Tensor
-    staging_ready: Any
+    # Two pinned staging copies of the plan, used in turn, each with the
+    # event of its last host-to-device copy.
+    plan_staging: list
+    staging_ready: list
     workspace: torch.Tensor
     output: torch.Tensor
     plan: Any = None
+    staging_turn: int = 0
 
     def views(self):
         """(counts, items, wave_extra, merges) views of the device plan buffer."""
@@ -443,6 +484,7 @@ class MI355XAttentionBackendMixin:
         self._output_buffer: torch.Tensor | None = None
         self._workspace: torch.Tensor | None = None
         self._prefill_workspace: torch.Tensor | None = None
+        self._staging = PinnedStaging()
         self._active_graph_state: MI355XFullDecodeGraphState | None = None
         # (key, value, slot_mapping) of the step while forward_with_kv_store
         # folds the KV store into the decode launch.
@@ -577,7 +619,7 @@ class MI355XAttentionBackendMixin:
             parts = [items.reshape(-1), merges.reshape(-1)]
             if wave_extra is not None:
                 parts.append(wave_extra)
-            flat = _to_device(np.concatenate(parts).astype(np.int32), block_tables.device)
+            flat = self._staging.to_device(np.concatenate(parts), block_tables.device)
             n_items, n_merge = num_decode_items * ops.DECODE_ITEM_INTS, num_decode_merges * ops.DECODE_ITEM_INTS
             decode_items = flat[:n_items].view(num_decode_items, ops.DECODE_ITEM_INTS)
             decode_merges = flat[n_items:n_items + n_merge].view(num_decode_merges, ops.DECODE_ITEM_INTS)
@@ -868,8 +910,8 @@ class MI355XAttentionBackendMixin:
             block_tables_buffer=torch.zeros((batch_size, width), dtype=torch.int32, device=graph_device),
             seq_lens_buffer=torch.ones(batch_size, dtype=torch.int32, device=graph_device),
             plan_buffer=torch.zeros(plan_ints, dtype=torch.int32, device=graph_device),
-            plan_staging=torch.zeros(plan_ints, dtype=torch.int32, pin_memory=True),
-            staging_ready=None,
+            plan_staging=[torch.zeros(plan_ints, dtype=torch.int32, pin_memory=True) for _ in range(2)],
+            staging_ready=[None, None],
             workspace=torch.zeros(ws_bytes, dtype=torch.uint8, device=graph_device),
             output=torch.empty(batch_size, self.num_q_heads, self.head_dim, dtype=self.dtype, device=graph_device),
             **caps,
@@ -922,15 +964,19 @@ class MI355XAttentionBackendMixin:
             merges = ops.decode_merge_list(items)
         else:
             items, wave_extra, merges, _ = host
-        # The previous step's copy must have read the staging buffer first.
-        if state.staging_ready is not None:
-            state.staging_ready.synchronize()
+        # Staging buffers alternate: the one refilled now was last copied two
+        # steps ago, so the host waits only if it runs two steps ahead.
+        k = state.staging_turn
+        state.staging_turn ^= 1
+        if state.staging_ready[k] is not None:
+            state.staging_ready[k].synchronize()
+        staging = state.plan_staging[k]
         pack_graph_decode_plan(items, wave_extra, merges, state.item_capacity, state.wave_capacity,
-                               state.merge_capacity, state.plan_staging.numpy())
-        state.plan_buffer.copy_(state.plan_staging, non_blocking=True)
+                               state.merge_capacity, staging.numpy())
+        state.plan_buffer.copy_(staging, non_blocking=True)
         event = torch.cuda.Event()
         event.record()
-        state.staging_ready = event
+        state.staging_ready[k] = event
         bt = metadata.block_tables
         state.block_tables_buffer[:, : bt.size(1)].copy_(bt)
         state.seq_lens_buffer.copy_(metadata.seq_lens)
@@ -989,7 +1035,7 @@ class MI355XAttentionBackendMixin:
         for s_idx, (base, c) in enumerate(zip(first_page, counts)):
             table[s_idx, :c] = np.arange(base, base + c)
         host = np.concatenate([slots, table.reshape(-1), q_lens]).astype(np.int32)
-        flat = _to_device(host, device)
+        flat = self._staging.to_device(host, device)
         n_slot, n_table = slots.size, table.size
         slot_mapping = flat[:n_slot]
         block_tables = flat[n_slot:n_slot + n_table].view(table.shape)

@@ -228,3 +228,23 @@ def test_backend_supports_this_gpu(gpu):
     caps = dict(num_q_heads=16, num_kv_heads=8, head_dim=128, block_size=16, dtype=torch.bfloat16, device=gpu)
     assert MI355XAttentionBackend.support_reason(**caps) is None
     assert MI355XAttentionBackend.supports(**caps) is True
+
+
+def test_one_backend_replans_many_steps_through_its_staging_ring(gpu):
+    # Nine decode steps of different batches planned back to back on one
+    # backend, without synchronizing: the work lists go through the
+    # backend's ring of pinned staging buffers (four), each reused only after
+    # its previous copy; every step's output matches the oracle.
+    backend = MI355XAttentionBackend(16, 8, 128, 16, torch.bfloat16)
+    steps = []
+    for k in range(9):
+        n = 3 + k
+        batch = make_paged_batch(400 + k, [1] * n, [40 + 97 * i + 13 * k for i in range(n)], 0, 16, 8)
+        common, q, kc, vc = _to(batch, gpu)
+        plan = backend.build_plan(common)
+        empty = q.new_empty((0, 8, 128))
+        out = backend.forward(q, empty, empty, kc, vc, plan).clone()
+        steps.append((batch, out))
+    torch.cuda.synchronize()
+    for batch, out in steps:
+        assert_attention_close(out, _expected(batch))
