@@ -401,6 +401,11 @@ def test_mixed_beyond_one_launch_limits_runs_as_two_launches():
     assert plan.metadata.mixed_prefill_max_tiles == 0 and plan.metadata.prefill_max_tiles > 0
     small = backend.build_plan(_common((5, 1), (21, 13), 1, trusted=True))
     assert small.metadata.mixed_prefill_max_tiles > 0
+    # More KV heads than one MIXED launch's counters cover: two launches too.
+    wide = HostBackend(128, 128, 128, 16, torch.bfloat16)
+    assert ops.MIXED_MAX_KV_HEADS < 128
+    plan = wide.build_plan(_common((5, 1), (21, 13), 1, trusted=True))
+    assert plan.route is AttentionRoute.MIXED_UNIFIED and plan.metadata.mixed_prefill_max_tiles == 0
 
 
 @pytest.mark.parametrize("seed", range(5))
