@@ -92,8 +92,9 @@ class MI355XAttentionMetadata:
     decode_host_plan: tuple | None = None
     # Bounds on the prefill query tiles (size the device-built tile list and
     # the MIXED launch's prefill pool).  mixed_prefill_max_tiles == 0 on a
-    # MIXED_UNIFIED plan: more prefill sequences or KV heads than one MIXED
-    # launch takes, so the batch runs as prefill + decode launches.
+    # MIXED_UNIFIED plan: more prefill sequences, KV heads or split-K
+    # segments than one MIXED launch takes, so the batch runs as prefill +
+    # decode launches.
     prefill_max_tiles: int = 0
     mixed_prefill_max_tiles: int = 0
 
@@ -592,24 +593,34 @@ class MI355XAttentionBackendMixin:
         num_decode_waves = 0
         num_part_slots = 0
         waves_per_group = 1
+        # A MIXED batch runs as one launch when it fits that launch's limits.
+        one_launch = bool(common.num_prefill_seqs and common.num_decode_seqs) and self._mixed_in_one_launch(common)
         if common.num_decode_seqs:
             decode_counts = counts[common.num_prefill_seqs:]
-            one_launch = bool(common.num_prefill_seqs) and self._mixed_in_one_launch(common)
             wave_extra = None
-            if not one_launch and decode_schedule(int(decode_counts.sum()), self.num_kv_heads) == "listed":
-                groups, waves_per_group = listed_decode_groups(self.num_kv_heads, block_tables.device)
-                items, wave_extra, num_decode_waves, num_part_slots = make_decode_plan_listed(
-                    decode_counts, common.num_prefill_seqs, common.num_prefill_tokens, self.num_kv_heads, groups
-                )
-            else:
-                waves = resident_decode_waves(block_tables.device, mixed=one_launch)
+            if one_launch:
                 items, num_decode_waves, num_part_slots = make_decode_plan(
-                    decode_counts,
-                    common.num_prefill_seqs,
-                    common.num_prefill_tokens,
-                    self.num_kv_heads,
-                    waves,
+                    decode_counts, common.num_prefill_seqs, common.num_prefill_tokens, self.num_kv_heads,
+                    resident_decode_waves(block_tables.device, mixed=True),
                 )
+                # Its split-K arrival counters cover a bounded number of
+                # (partial slot, KV head) pairs.
+                if num_part_slots * self.num_kv_heads > ops.MIXED_ARRIVAL_COUNTERS:
+                    one_launch = False
+            if not one_launch:
+                if decode_schedule(int(decode_counts.sum()), self.num_kv_heads) == "listed":
+                    groups, waves_per_group = listed_decode_groups(self.num_kv_heads, block_tables.device)
+                    items, wave_extra, num_decode_waves, num_part_slots = make_decode_plan_listed(
+                        decode_counts, common.num_prefill_seqs, common.num_prefill_tokens, self.num_kv_heads, groups
+                    )
+                else:
+                    items, num_decode_waves, num_part_slots = make_decode_plan(
+                        decode_counts,
+                        common.num_prefill_seqs,
+                        common.num_prefill_tokens,
+                        self.num_kv_heads,
+                        resident_decode_waves(block_tables.device),
+                    )
             # The single MIXED launch merges split segments itself.
             merges = np.zeros((0, ops.DECODE_ITEM_INTS), np.int32) if one_launch else ops.decode_merge_list(items)
             num_decode_items = items.shape[0]
@@ -631,7 +642,7 @@ class MI355XAttentionBackendMixin:
         if common.num_prefill_seqs:
             prefill_max_tiles = ops.prefill_max_tiles(common.num_prefill_tokens, common.num_prefill_seqs,
                                                       self.num_q_heads, self.num_kv_heads)
-            if common.num_decode_seqs and self._mixed_in_one_launch(common):
+            if one_launch:
                 mixed_prefill_max_tiles = ops.mixed_prefill_max_tiles(
                     common.num_prefill_tokens, common.num_prefill_seqs, self.num_q_heads, self.num_kv_heads
                 )

@@ -292,6 +292,13 @@ constexpr int kMixedPrefillCtrInt = (kDecodeClaimCounters + 2) * kDecodeSchedLin
 constexpr int kMixedPrefillExitOffset = 16;
 static_assert((kMixedPrefillCtrInt + kMixedPrefillMaxHeads * kDecodeSchedLineInts) * 4 <= kDecodeSchedBytes,
               "MIXED prefill counters");
+// MIXED launches merge split-K segments themselves: one arrival counter per
+// (partial slot, KV head), in a fixed region right after the scheduler area.
+// No other kernel writes there, and the last arrival of a segment clears its
+// counter, so the counters are zero at every MIXED launch whatever plans
+// (and partial layouts) used the workspace in between.
+constexpr int kArrivalCounters = 65536;
+constexpr int64_t kArrivalBytes = (int64_t)kArrivalCounters * 4;
 
 template <typename T, bool kAgent>
 __device__ void merge_segment(const DecodeParams& p, const i32x8& d, int g);

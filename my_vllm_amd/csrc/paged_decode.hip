@@ -68,18 +68,15 @@ int launch_decode_merge(const DecodeParams& p, const int32_t* merges, int64_t nu
 
 static int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
-// Workspace layout: [scheduler (kDecodeSchedBytes)][lse f32 slots*Hkv*G]
-// [o f32 slots*Hkv*G*D][arrival counters i32 slots*Hkv (MIXED launches)].
+// Workspace layout: [scheduler (kDecodeSchedBytes)][arrival counters
+// (kArrivalBytes, MIXED launches)][lse f32 slots*Hkv*G][o f32 slots*Hkv*G*D].
 int64_t decode_workspace_bytes(int64_t slots, int hkv, int group) {
-  return kDecodeSchedBytes + align256(slots * hkv * group * 4) + align256(slots * hkv * group * kHeadDim * 4) +
-         align256(slots * hkv * 4);
+  return kDecodeSchedBytes + kArrivalBytes + align256(slots * hkv * group * 4) +
+         align256(slots * hkv * group * kHeadDim * 4);
 }
 
 // The arrival counters of a workspace laid out as above.
-int32_t* decode_arrival_counters(void* workspace, int64_t slots, int hkv, int group) {
-  return (int32_t*)((uint8_t*)workspace + kDecodeSchedBytes + align256(slots * hkv * group * 4) +
-                    align256(slots * hkv * group * kHeadDim * 4));
-}
+int32_t* decode_arrival_counters(void* workspace) { return (int32_t*)((uint8_t*)workspace + kDecodeSchedBytes); }
 
 int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, int64_t q_head_stride,
                        const void* k_cache, const void* v_cache, int64_t num_pages, int64_t page_stride,
@@ -139,7 +136,7 @@ int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, i
   p.slots = nullptr;
   p.num_new = 0;
   p.sched = (int32_t*)ws;
-  ws += kDecodeSchedBytes;
+  ws += kDecodeSchedBytes + kArrivalBytes;
   p.part_lse = (float*)ws;
   ws += align256(num_part_slots * num_kv_heads * group * 4);
   p.part_o = (float*)ws;

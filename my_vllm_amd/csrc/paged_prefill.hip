@@ -17,7 +17,7 @@ int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, i
                        float softmax_scale);
 int launch_decode_merge(const DecodeParams& p, const int32_t* merges, int64_t num_merges, int dtype,
                         hipStream_t stream);
-int32_t* decode_arrival_counters(void* workspace, int64_t slots, int hkv, int group);
+int32_t* decode_arrival_counters(void* workspace);
 
 namespace {
 
@@ -471,7 +471,9 @@ extern "C" int mva_paged_mixed(const void* q, int64_t q_token_stride, int64_t q_
                           softmax_scale);
   if (rc) return rc;
   // Split-K segments are merged inside the launch by their last piece.
-  dp.arrive = decode_arrival_counters(workspace, num_part_slots, num_kv_heads, dp.group);
+  if (num_part_slots * num_kv_heads > kArrivalCounters)
+    return set_error("paged attention: a MIXED launch takes at most 65536 split-K (partial slot, KV head) pairs");
+  dp.arrive = decode_arrival_counters(workspace);
   // Prefill pool: two workgroups per CU (the CU's eight wave slots), a whole
   // number per KV head, never more than the tiles can use.
   int64_t per_head = 0;

@@ -552,6 +552,9 @@ def mixed_prefill_max_tiles(num_prefill_tokens: int, num_prefill_seqs: int, num_
 # kMixedPrefillMaxHeads); larger MIXED batches run as prefill + decode.
 MIXED_PREFILL_SEQS_MAX = 1024
 MIXED_MAX_KV_HEADS = 64
+# Split-K (partial slot, KV head) pairs one MIXED launch merges
+# (kArrivalCounters).
+MIXED_ARRIVAL_COUNTERS = 65536
 
 
 def prefill_workspace_bytes(max_tiles: int) -> int:

@@ -162,3 +162,32 @@ def test_mixed_beyond_one_launch_runs_prefill_then_decode(gpu):
     out, plan = run_backend(batch, gpu)
     assert plan.route is AttentionRoute.MIXED_UNIFIED and plan.metadata.mixed_prefill_max_tiles == 0
     assert_attention_close(out, expected(batch))
+
+
+def test_mixed_after_decode_steps_on_one_workspace(gpu, monkeypatch):
+    # A decode step with many split-K partial slots, then MIXED steps with
+    # fewer, then a decode step, all on one backend and workspace: the MIXED
+    # launch's arrival counters must not see the earlier partials, and every
+    # step matches the oracle.
+    from my_vllm_amd.attention_backend import MI355XAttentionBackend
+    from tests.test_gpu_prefill import to_device
+
+    backend = MI355XAttentionBackend(32, 8, 128, 16, torch.bfloat16)
+    batches = [
+        make_paged_batch(111, [1] * 40, [1500 + 37 * i for i in range(40)], 0, 32, 8),
+        make_paged_batch(112, [30, 1, 1, 1], [300, 900, 2100, 40], 1, 32, 8),
+        make_paged_batch(113, [7, 20, 1, 1], [7, 500, 3000, 1000], 2, 32, 8),
+        make_paged_batch(114, [1] * 12, [800 + 90 * i for i in range(12)], 0, 32, 8),
+    ]
+    for b in batches:
+        # Default decode planning (many ranges, many partial slots); few
+        # decode wavefronts in the MIXED launches (few partial slots).
+        if b.common.num_prefill_seqs:
+            monkeypatch.setenv("MVA_DECODE_WAVES", "64")
+        else:
+            monkeypatch.delenv("MVA_DECODE_WAVES", raising=False)
+        common, qd, kc, vc = to_device(b, gpu)
+        plan = backend.build_plan(common)
+        empty = qd.new_empty((0, 8, 128))
+        out = backend.forward(qd, empty, empty, kc, vc, plan)
+        assert_attention_close(out, expected(b))
