@@ -59,10 +59,12 @@ def test_qwen3_8b_mixed_configuration(gpu):
 
 
 @pytest.mark.parametrize("mode", ["unified", "split"])
-@pytest.mark.parametrize("hq,hkv", [(8, 8), (12, 4), (64, 8)])
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (12, 4), (64, 8), (6, 3), (16, 1)])
 def test_mixed_gqa_ratios(gpu, mode, hq, hkv):
-    # G = 1, 3 and 8: the prefill tile of one launch holds 128 // G tokens of
-    # every query head of a KV head; decode wavefronts cover G heads each.
+    # G = 1, 3, 8, 2 and 16: the prefill tile of one launch holds 128 // G
+    # tokens of every query head of a KV head; decode wavefronts cover G heads
+    # each.  3 and 1 KV heads give prefill pools that are not a multiple of
+    # the 8 XCDs.
     batch = make_paged_batch(97, [70, 33, 1, 1, 1], [70, 290, 9, 700, 2100], 2, hq, hkv)
     out, plan = run_backend(batch, gpu, mode=mode)
     assert plan.batch_type is BatchType.MIXED
