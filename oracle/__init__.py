@@ -3,7 +3,7 @@
 A restatement, in plain torch/numpy on the CPU, of the reference's native
 (non-FlashInfer) arithmetic for each kernel of this repository.  Only
 ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg may
-import it, and only as the checker or the timed CPU baseline: the product
+import it, and only to check results or as the timed CPU baseline: the product
 package (``my_vllm_amd``) never imports it and has no CPU fallback.
 
 How each function is pinned (the tests under ``tests/test_oracle*.py``):
