@@ -9,7 +9,7 @@ random permutation of a pool sized to the total context.  Every sequence's
 ``[seq_len - q_len, seq_len)``.  Prefill sequences come first.
 
 Values are drawn from N(0, 1) with a seeded ``torch.Generator``.  Small batches
-are drawn on the CPU (so a CPU checker sees identical bits); multi-GB batches
+are drawn on the CPU (so the CPU oracle sees identical bits); multi-GB batches
 can be drawn directly on the GPU (``rng_device="cuda"``).
 """
 
