@@ -36,8 +36,8 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* __res
                                                             int tile_tokens, int num_kv_heads,
                                                             int32_t* __restrict__ plan, int capacity) {
   // Sequences in plan order (rank -> sequence) and the first tile of each
-  // rank; sequences beyond kPrefillPlanSortMax keep batch order and are
-  // planned in later rounds of the same steps.
+  // rank; beyond kPrefillPlanSortMax sequences, all keep batch order and are
+  // planned in passes of kPrefillPlanSortMax.
   __shared__ int kv_of[kPrefillPlanSortMax];
   __shared__ int order[kPrefillPlanSortMax];
   __shared__ int first_tile[kPrefillPlanSortMax + 1];
@@ -63,7 +63,8 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* __res
   int32_t* out = plan + kPrefillPlanHeaderInts;
   for (int c = 0; c < num_seqs; c += kPrefillPlanSortMax) {
     const int span = min(kPrefillPlanSortMax, num_seqs - c);
-    // Tiles per rank in this round, then their exclusive prefix sum.
+    // Tiles per rank in this pass over the sequences, then their exclusive
+    // prefix sum.
     for (int r0 = 0; r0 < span; r0 += 1024) {
       const int r = r0 + tid;
       int nt = 0;
