@@ -433,8 +433,8 @@ constexpr int kPrefillPlanItemInts = 16;
 constexpr int kPrefillPlanLineInts = 32;
 constexpr int kPrefillPlanMaxHeads = 127;
 constexpr int kPrefillPlanHeaderInts = kPrefillPlanLineInts * (1 + kPrefillPlanMaxHeads);
-// Sequences the planner sorts longest-context first (more are planned in
-// batch order).
+// Largest batch the planner sorts longest-context first (a larger batch is
+// planned in batch order).
 constexpr int kPrefillPlanSortMax = 2048;
 
 // The tile list mva_paged_prefill builds on the device: the record of tile

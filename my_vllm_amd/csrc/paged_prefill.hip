@@ -23,8 +23,9 @@ namespace {
 
 // Exact tile list of a prefill batch, built on the device from
 // query_start_loc / seq_lens (one workgroup; see kPrefillPlanHeaderInts for
-// the format).  Sequences are ordered longest context first (up to
-// kPrefillPlanSortMax sequences; batch order beyond), and a sequence's tiles
+// the format).  Sequences are ordered longest context first (batches of up
+// to kPrefillPlanSortMax sequences; larger batches keep batch order), and a
+// sequence's tiles
 // largest key count first, so the tiles that read one sequence's pages run
 // together and long work starts early.  A sequence with no queries, or with
 // more queries than keys, gets no tile.  At most `capacity` tiles are
