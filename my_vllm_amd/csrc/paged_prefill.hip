@@ -26,9 +26,9 @@ namespace {
 // the format).  Sequences are ordered longest context first (batches of up
 // to kPrefillPlanSortMax sequences; larger batches keep batch order), and a
 // sequence's tiles largest key count first, so the tiles that read one
-// sequence's pages run together and long work starts early.  A sequence with no queries, or with
-// more queries than keys, gets no tile.  At most `capacity` tiles are
-// written; word 0 receives their number.
+// sequence's pages run together and long work starts early.  A sequence
+// with no queries, or with more queries than keys, gets no tile.  At most
+// `capacity` tiles are written; word 0 receives their number.
 __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* __restrict__ qsl,
                                                             const int32_t* __restrict__ seq_lens,
                                                             const int32_t* __restrict__ block_tables,
