@@ -193,3 +193,33 @@ def test_mixed_after_decode_steps_on_one_workspace(gpu, monkeypatch):
         empty = qd.new_empty((0, 8, 128))
         out = backend.forward(qd, empty, empty, kc, vc, plan)
         assert_attention_close(out, expected(b))
+
+
+def test_many_launches_keep_the_counters_consistent(gpu):
+    # 120 back-to-back launches on one backend: MIXED (prefill pool claims,
+    # in-launch merges), DECODE (claim counters, merge kernel) and PREFILL in
+    # turn; the counters each launch leaves at zero are what the next one
+    # starts from, so every output must stay equal to its first.
+    from my_vllm_amd.attention_backend import MI355XAttentionBackend
+    from tests.test_gpu_prefill import to_device
+
+    backend = MI355XAttentionBackend(32, 8, 128, 16, torch.bfloat16)
+    batches = [
+        make_paged_batch(121, [64, 9, 1, 1, 1], [300, 9, 1500, 40, 2600], 2, 32, 8),
+        make_paged_batch(122, [1] * 20, [100 + 150 * i for i in range(20)], 0, 32, 8),
+        make_paged_batch(123, [200, 31], [700, 31], 2, 32, 8),
+    ]
+    steps = []
+    for b in batches:
+        common, qd, kc, vc = to_device(b, gpu)
+        plan = backend.build_plan(common)
+        steps.append((qd, kc, vc, plan))
+    empty = steps[0][0].new_empty((0, 8, 128))
+    firsts = [backend.forward(qd, empty, empty, kc, vc, plan).clone() for qd, kc, vc, plan in steps]
+    for i in range(120):
+        qd, kc, vc, plan = steps[i % 3]
+        out = backend.forward(qd, empty, empty, kc, vc, plan)
+        if i % 30 < 3:
+            assert torch.equal(out, firsts[i % 3]), f"launch {i} differs"
+    for b, first in zip(batches, firsts):
+        assert_attention_close(first, expected(b))
