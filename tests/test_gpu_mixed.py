@@ -223,3 +223,14 @@ def test_many_launches_keep_the_counters_consistent(gpu):
             assert torch.equal(out, firsts[i % 3]), f"launch {i} differs"
     for b, first in zip(batches, firsts):
         assert_attention_close(first, expected(b))
+
+
+def test_mixed_untrusted_metadata_matches_trusted(gpu):
+    # The untrusted path validates the metadata on the device side first;
+    # the launch itself is the same, so the rows are bit-identical.
+    batch = make_paged_batch(125, [40, 300, 1, 1], [100, 300, 70, 900], 2, 32, 8)
+    a, _ = run_backend(batch, gpu, trusted=True)
+    a = a.clone()
+    b, plan = run_backend(batch, gpu, trusted=False)
+    assert plan.route is AttentionRoute.MIXED_UNIFIED
+    assert torch.equal(a, b)
