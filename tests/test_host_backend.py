@@ -479,3 +479,15 @@ def test_graph_hooks_validate_like_the_reference():
     with pytest.raises(TypeError):
         backend.activate_full_decode_graph(object())
     backend.deactivate_full_decode_graph()
+
+
+def test_pinned_staging_round_trips_int32_lists_on_the_host():
+    from my_vllm_amd.attention_backend import PinnedStaging
+
+    ring = PinnedStaging(slots=2)
+    rng = np.random.default_rng(5)
+    for n in (0, 1, 7, 5000, 3):
+        a = rng.integers(-(2**31), 2**31 - 1, size=n, dtype=np.int64).astype(np.int32)
+        t = ring.to_device(a, torch.device("cpu"))
+        assert t.dtype == torch.int32 and t.shape == (n,)
+        assert np.array_equal(t.numpy(), a)
