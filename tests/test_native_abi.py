@@ -67,6 +67,10 @@ def test_invalid_arguments_fail_before_launch_with_a_message():
     with pytest.raises(RuntimeError, match="mva_paged_decode failed"):
         _native.call("mva_paged_decode", 0, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0, 1, 1, 0, 1, 0, 0, 0, 0, 0, 0, 0, 0,
                      16, 8, 64, 16, 1.0, 0, 0)
+    # A MIXED launch orders at most 1024 prefill sequences in LDS.
+    with pytest.raises(RuntimeError, match="at most 1024 prefill sequences"):
+        _native.call("mva_paged_mixed", 0, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0, 1025, 2000, 0, 0, 0, 0,
+                     0, 0, 0, 0, 0, 16, 8, 128, 16, 1.0, 0, 0)
 
 
 def test_dtype_codes_match_the_header():
