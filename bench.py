@@ -20,7 +20,7 @@ stream).  Prefill and MIXED inputs are the CPU-seeded draws the parity tests
 check; the 10.7 GB long-decode batch is drawn on the GPU, as its test does.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra]
-       python bench.py --only {decode,decode_store,long_decode,prefill,mixed,silu,store,copy} [--steps K]
+       python bench.py --only {decode,decode_store,long_decode,prefill,mixed,silu,store,rms,prologue,copy} [--steps K]
 The ``--only`` forms run one workload's kernel K times and print one line;
 they are the programs the committed rocprofv3 summaries profile (``copy`` is
 a 256 MiB device copy used to calibrate the byte counters).
@@ -52,6 +52,7 @@ def parse_args(argv=None):
     ap.add_argument("--no-extra", action="store_true", help="headline and roofline only")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--only", choices=["decode", "decode_store", "long_decode", "prefill", "mixed", "silu", "store",
+                                       "rms", "prologue",
                                        "copy"],
                     help="run one workload's kernel --steps times (for profilers) and exit")
     return ap.parse_args(argv)
@@ -345,6 +346,15 @@ def extra_measurements(device, steps: int):
     return res
 
 
+def prologue_bytes(tokens: int, hq: int, hkv: int) -> int:
+    """Algorithmic HBM bytes of one fused prologue launch: read each q, k and v
+    row once; write q and k back in place and k and v into the cache (bf16,
+    128 per row)."""
+    rows_read = hq + 2 * hkv
+    rows_written = (hq + hkv) + 2 * hkv
+    return tokens * (rows_read + rows_written) * 128 * 2
+
+
 def prologue_fused_vs_separate(device, tokens: int = 4096, hq: int = 32, hkv: int = 8):
     """Attention prologue at the Qwen3-8B shape for a 4096-token chunk: q/k
     RMSNorm + RoPE + KV store as one launch vs the four separate ops."""
@@ -377,7 +387,7 @@ def prologue_fused_vs_separate(device, tokens: int = 4096, hq: int = 32, hkv: in
 
     fused_ms = time_launches(fused, 200, 20)
     sep_ms = time_launches(separate, 200, 20)
-    moved = tokens * (hq + 2 * hkv) * 128 * 2 * 2  # read and write each q/k/v row once
+    moved = prologue_bytes(tokens, hq, hkv)
     return {"prologue_4096tok_fused_us": round(fused_ms * 1e3, 2),
             "prologue_4096tok_separate_us": round(sep_ms * 1e3, 2),
             "prologue_4096tok_fused_GBps": round(moved / fused_ms / 1e6, 1)}
@@ -465,6 +475,43 @@ def run_only(args, device):
             ops.silu_and_mul(xs[i % 8])
         torch.cuda.synchronize()
         print(json.dumps({"only": "silu", "bytes_per_launch": 75497472, "launches": n, "rotated_inputs": 8}))
+        return 0
+    if args.only == "rms":
+        # Fused residual-add RMSNorm, 4096 x 4096 (Qwen3-8B hidden), 8 rotated
+        # input / residual pairs (512 MB, past the 256 MB Infinity Cache).
+        xs = [silu_input(4096, 4096, seed=10 + i, device=device, rng_device="cuda") for i in range(8)]
+        rs = [silu_input(4096, 4096, seed=20 + i, device=device, rng_device="cuda") for i in range(8)]
+        w = torch.ones(4096, dtype=torch.bfloat16, device=device)
+        for i in range(n):
+            ops.fused_add_rms_norm(xs[i % 8], rs[i % 8], w, 1e-6)
+        torch.cuda.synchronize()
+        print(json.dumps({"only": "rms", "bytes_per_launch": 4 * 4096 * 4096 * 2, "launches": n,
+                          "rotated_inputs": 8}))
+        return 0
+    if args.only == "prologue":
+        # Fused q/k-RMSNorm + RoPE + KV store, 4096 tokens at Qwen3-8B heads
+        # (32 Q / 8 KV), 6 rotated qkv buffers (300 MB, past the Infinity Cache).
+        from my_vllm_amd.custom_op import CustomOpConfig
+        from my_vllm_amd.layers import RotaryEmbedding
+
+        tokens, hq, hkv = 4096, 32, 8
+        width = (hq + 2 * hkv) * 128
+        qkvs = [silu_input(tokens, width, seed=30 + i, device=device, rng_device="cuda") for i in range(6)]
+        pos = torch.arange(tokens, device=device, dtype=torch.int64)
+        table = RotaryEmbedding(128, 128, 40960, 1e6, CustomOpConfig(platform="cuda")).cos_sin_cache.to(device)
+        w = torch.ones(128, dtype=torch.bfloat16, device=device)
+        kc = torch.zeros(tokens // 16, 16, hkv, 128, dtype=torch.bfloat16, device=device)
+        vc = torch.zeros_like(kc)
+        slots = torch.arange(tokens, dtype=torch.int32, device=device)
+        for i in range(n):
+            qkv = qkvs[i % 6]
+            q = qkv[:, : hq * 128].view(tokens, hq, 128)
+            k = qkv[:, hq * 128:(hq + hkv) * 128].view(tokens, hkv, 128)
+            v = qkv[:, (hq + hkv) * 128:].view(tokens, hkv, 128)
+            ops.qk_norm_rope_store(pos, q, k, table, w, w, 1e-6, v, kc, vc, slots)
+        torch.cuda.synchronize()
+        print(json.dumps({"only": "prologue", "bytes_per_launch": prologue_bytes(tokens, hq, hkv),
+                          "launches": n, "rotated_inputs": 6}))
         return 0
     if args.only == "store":
         # 16384 new tokens (a 16K-token prefill chunk) at 8 KV heads, scattered

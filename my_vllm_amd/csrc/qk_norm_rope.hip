@@ -74,13 +74,25 @@ __device__ inline f32x4v load_w4(const void* w, int i) {
   }
 }
 
-// Four (token, head) rows per wavefront: the 16 lanes of group g = lane / 16
-// own row 4q + g of the current quad q; lane c = lane % 16 holds elements
-// 4c .. 4c+3 of the first half of the head and 64 + 4c .. 64 + 4c + 3 of the
-// second (the pairs the rotation mixes), loaded and stored 8 bytes at a time.
 // Rows r of a token: [0, Hq) queries, [Hq, Hq + Hkv) keys, then (with a
-// store) [Hq + Hkv, Hq + 2 Hkv) values.  A grid-stride loop over quads.
-template <typename T, typename W>
+// store) [Hq + Hkv, Hq + 2 Hkv) values; a quad is four consecutive rows.
+// Within a quad the 16 lanes of group g = lane / 16 own row 4q + g; lane
+// c = lane % 16 holds elements 4c .. 4c+3 of the first half of the head and
+// 64 + 4c .. 64 + 4c + 3 of the second (the pairs the rotation mixes),
+// loaded and stored 8 bytes at a time.
+//
+// A wavefront takes one item at a time: up to kChunk quads of one token.
+// The token is uniform over the wavefront, so its position and slot are
+// two loads, and the item issues them, then every row load, then (once the
+// position is in) the one cos / sin row all its rows share: two memory
+// round trips per item.  Written row by row, each row would wait on the
+// position, then the cos / sin row, then the data, and the compiler cannot
+// hoist the next row's loads above this row's stores, since the outputs
+// may alias the inputs.  Distinct rows never overlap, so reading an item's
+// rows before writing any of them is exact even in place.
+constexpr int kChunk = 6;
+
+template <typename T, typename W, typename SlotT>
 __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(PrologueArgs a) {
   // Separate fp32 multiplies and adds, as torch evaluates the rotation (no
   // fused multiply-add contraction).
@@ -89,90 +101,125 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(PrologueArgs a)
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4;
   const int c4 = 4 * (lane & 15);
-  const int rows_per_tok = a.num_q_heads + a.num_kv_heads + (a.k_cache != nullptr ? a.num_kv_heads : 0);
-  const int64_t total = a.num_tokens * rows_per_tok;
+  const int hqk = a.num_q_heads + a.num_kv_heads;
+  const bool store = a.k_cache != nullptr;
+  const int R = hqk + (store ? a.num_kv_heads : 0);
+  const int nq = (R + 3) / 4;
+  const int S = (nq + kChunk - 1) / kChunk;  // items per token
   const int64_t waves = (int64_t)gridDim.x * 4;
-  for (int64_t quad = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); quad * 4 < total; quad += waves) {
-    const int64_t row = quad * 4 + g;
-    if (row >= total) continue;  // a whole 16-lane group: no shuffle partner is lost
-    const int64_t t = row / rows_per_tok;
-    const int r = (int)(row - t * rows_per_tok);
-    int64_t slot = -1;
-    if (a.k_cache != nullptr) {
-      slot = a.slot_is_int64 ? ((const int64_t*)a.slots)[t] : (int64_t)((const int32_t*)a.slots)[t];
-      if (slot >= a.num_slots) slot = -1;
-    }
-    const int64_t cache_row = (slot >= 0) ? slot * a.num_kv_heads : 0;  // rows of [slots * Hkv, 128]
-    if (r >= a.num_q_heads + a.num_kv_heads) {  // V: copy into the cache
-      if (slot >= 0) {
-        const int h = r - a.num_q_heads - a.num_kv_heads;
-        const T* src = (const T*)a.v + t * a.v_tok_stride + h * a.v_head_stride;
-        T* dst = (T*)a.v_cache + (cache_row + h) * kRopeDim;
-        *reinterpret_cast<V4*>(dst + c4) = *reinterpret_cast<const V4*>(src + c4);
-        *reinterpret_cast<V4*>(dst + 64 + c4) = *reinterpret_cast<const V4*>(src + 64 + c4);
-      }
-      continue;
-    }
-    const bool is_q = r < a.num_q_heads;
-    const int h = is_q ? r : r - a.num_q_heads;
-    const T* src = is_q ? (const T*)a.q_in + t * a.q_tok_stride + h * a.q_head_stride
-                        : (const T*)a.k_in + t * a.k_tok_stride + h * a.k_head_stride;
-    const V4 lo = *reinterpret_cast<const V4*>(src + c4);
-    const V4 hi = *reinterpret_cast<const V4*>(src + 64 + c4);
-    float x1[4], x2[4];
+  const bool norm = a.q_norm_w != nullptr;
+  f32x4v wq1{}, wq2{}, wk1{}, wk2{};
+  if (norm) {
+    wq1 = load_w4<W>(a.q_norm_w, c4);
+    wq2 = load_w4<W>(a.q_norm_w, 64 + c4);
+    wk1 = load_w4<W>(a.k_norm_w, c4);
+    wk2 = load_w4<W>(a.k_norm_w, 64 + c4);
+  }
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  for (int64_t it = (int64_t)blockIdx.x * 4 + wave; it < a.num_tokens * S; it += waves) {
+    const int64_t t = it / S;
+    const int j0 = (int)(it - t * S) * kChunk;  // this item's quads [j0, j0 + kChunk) within [0, nq)
+    // Without a store the slot pointer is the positions (a valid int64
+    // array of the same length) and the value goes unused.
+    const int64_t pos_in = a.positions[t];
+    const int64_t slot_in = (int64_t)((const SlotT*)a.slots)[t];
+    V4 lo[kChunk], hi[kChunk];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      x1[e] = (float)lo[e];
-      x2[e] = (float)hi[e];
+    for (int k = 0; k < kChunk; ++k) {
+      int r = 4 * (j0 + k) + g;
+      r = r < R ? r : 0;  // rows past the token read row 0 and are not written
+      const T* src;
+      if (r >= hqk)
+        src = (const T*)a.v + t * a.v_tok_stride + (r - hqk) * a.v_head_stride;
+      else if (r < a.num_q_heads)
+        src = (const T*)a.q_in + t * a.q_tok_stride + r * a.q_head_stride;
+      else
+        src = (const T*)a.k_in + t * a.k_tok_stride + (r - a.num_q_heads) * a.k_head_stride;
+      lo[k] = *reinterpret_cast<const V4*>(src + c4);
+      hi[k] = *reinterpret_cast<const V4*>(src + 64 + c4);
     }
-    const void* w = is_q ? a.q_norm_w : a.k_norm_w;
-    if (w != nullptr) {
-      float ss = 0.f;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ss += x1[e] * x1[e] + x2[e] * x2[e];
-#pragma unroll
-      for (int off = 8; off > 0; off >>= 1) ss += __shfl_xor(ss, off);  // within the 16-lane group
-      const float rr = 1.0f / __builtin_sqrtf(ss / (float)kRopeDim + a.eps);
-      const f32x4v w1 = load_w4<W>(w, c4);
-      const f32x4v w2 = load_w4<W>(w, 64 + c4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        x1[e] = (float)(T)((float)(T)(x1[e] * rr) * w1[e]);
-        x2[e] = (float)(T)((float)(T)(x2[e] * rr) * w2[e]);
-      }
-    }
-    int64_t pos = a.positions[t];
-    pos = pos < 0 ? 0 : (pos >= a.max_position ? a.max_position - 1 : pos);  // stay in bounds
+    const int64_t pos = pos_in < 0 ? 0 : (pos_in >= a.max_position ? a.max_position - 1 : pos_in);  // stay in bounds
     const f32x4v cs = *reinterpret_cast<const f32x4v*>(a.cos_sin + pos * kRopeDim + c4);
     const f32x4v sn = *reinterpret_cast<const f32x4v*>(a.cos_sin + pos * kRopeDim + 64 + c4);
-    V4 y1, y2;
+    const int64_t slot = (store && slot_in < a.num_slots) ? slot_in : -1;  // negative: skipped
+    const int64_t cache_row = (slot >= 0) ? slot * a.num_kv_heads : 0;  // rows of [slots * Hkv, 128]
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      y1[e] = (T)(x1[e] * cs[e] - x2[e] * sn[e]);
-      y2[e] = (T)(x2[e] * cs[e] + x1[e] * sn[e]);
+    for (int k = 0; k < kChunk; ++k) {
+      const int r = 4 * (j0 + k) + g;
+      if (r >= R) continue;  // a whole 16-lane group: no shuffle partner is lost
+      if (r >= hqk) {  // V: copy into the cache
+        if (slot >= 0) {
+          T* dst = (T*)a.v_cache + (cache_row + r - hqk) * kRopeDim;
+          *reinterpret_cast<V4*>(dst + c4) = lo[k];
+          *reinterpret_cast<V4*>(dst + 64 + c4) = hi[k];
+        }
+        continue;
+      }
+      const bool is_q = r < a.num_q_heads;
+      const int h = is_q ? r : r - a.num_q_heads;
+      float x1[4], x2[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x1[e] = (float)lo[k][e];
+        x2[e] = (float)hi[k][e];
+      }
+      if (norm) {
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ss += x1[e] * x1[e] + x2[e] * x2[e];
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1) ss += __shfl_xor(ss, off);  // within the 16-lane group
+        const float rs = 1.0f / __builtin_sqrtf(ss / (float)kRopeDim + a.eps);
+        const f32x4v w1 = is_q ? wq1 : wk1;
+        const f32x4v w2 = is_q ? wq2 : wk2;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x1[e] = (float)(T)((float)(T)(x1[e] * rs) * w1[e]);
+          x2[e] = (float)(T)((float)(T)(x2[e] * rs) * w2[e]);
+        }
+      }
+      V4 y1, y2;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        y1[e] = (T)(x1[e] * cs[e] - x2[e] * sn[e]);
+        y2[e] = (T)(x2[e] * cs[e] + x1[e] * sn[e]);
+      }
+      T* dst = is_q ? (T*)a.q_out + t * a.q_tok_stride + h * a.q_head_stride
+                    : (T*)a.k_out + t * a.k_tok_stride + h * a.k_head_stride;
+      *reinterpret_cast<V4*>(dst + c4) = y1;
+      *reinterpret_cast<V4*>(dst + 64 + c4) = y2;
+      if (!is_q && slot >= 0) {
+        T* kd = (T*)a.k_cache + (cache_row + h) * kRopeDim;
+        *reinterpret_cast<V4*>(kd + c4) = y1;
+        *reinterpret_cast<V4*>(kd + 64 + c4) = y2;
+      }
     }
-    T* dst = is_q ? (T*)a.q_out + t * a.q_tok_stride + h * a.q_head_stride
-                  : (T*)a.k_out + t * a.k_tok_stride + h * a.k_head_stride;
-    *reinterpret_cast<V4*>(dst + c4) = y1;
-    *reinterpret_cast<V4*>(dst + 64 + c4) = y2;
-    if (!is_q && slot >= 0) {
-      T* kd = (T*)a.k_cache + (cache_row + h) * kRopeDim;
-      *reinterpret_cast<V4*>(kd + c4) = y1;
-      *reinterpret_cast<V4*>(kd + 64 + c4) = y2;
-    }
+  }
+}
+
+template <typename T, typename W>
+void launch_prologue_kernel(PrologueArgs a, int64_t blocks, hipStream_t s) {
+  if (a.k_cache == nullptr) {
+    a.slots = a.positions;
+    hipLaunchKernelGGL((qk_norm_rope_store_kernel<T, W, int64_t>), dim3((uint32_t)blocks), dim3(256), 0, s, a);
+  } else if (a.slot_is_int64) {
+    hipLaunchKernelGGL((qk_norm_rope_store_kernel<T, W, int64_t>), dim3((uint32_t)blocks), dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((qk_norm_rope_store_kernel<T, W, int32_t>), dim3((uint32_t)blocks), dim3(256), 0, s, a);
   }
 }
 
 template <typename T>
 int launch_prologue(const PrologueArgs& a, int weight_dtype, hipStream_t s) {
-  const int64_t rows = a.num_tokens * (a.num_q_heads + a.num_kv_heads + (a.k_cache != nullptr ? a.num_kv_heads : 0));
-  const int64_t quads = (rows + 3) / 4;
-  // Four quads per workgroup pass; at most 8 resident workgroups per CU's worth.
-  const int64_t blocks = std::min<int64_t>((quads + 3) / 4, 256 * 16);
+  const int rows = a.num_q_heads + a.num_kv_heads + (a.k_cache != nullptr ? a.num_kv_heads : 0);
+  const int64_t items = a.num_tokens * (((rows + 3) / 4 + kChunk - 1) / kChunk);
+  // Four wavefronts per workgroup; at most 16 workgroups per CU's worth,
+  // beyond which the wavefronts loop.
+  const int64_t blocks = std::min<int64_t>((items + 3) / 4, 256 * 16);
   if (weight_dtype == kF32)
-    hipLaunchKernelGGL((qk_norm_rope_store_kernel<T, float>), dim3((uint32_t)blocks), dim3(256), 0, s, a);
+    launch_prologue_kernel<T, float>(a, blocks, s);
   else
-    hipLaunchKernelGGL((qk_norm_rope_store_kernel<T, T>), dim3((uint32_t)blocks), dim3(256), 0, s, a);
+    launch_prologue_kernel<T, T>(a, blocks, s);
   return check_launch("qk_norm_rope_store");
 }
 
