@@ -203,6 +203,7 @@ def qk_norm_rope_store(
         raise ValueError("positions must be int64 [tokens] and key must have the query's token count")
     if positions.device != device:
         raise ValueError("positions must be on the query device")
+    positions = positions.contiguous()  # the kernel indexes it densely
     table = cos_sin_cache.reshape(cos_sin_cache.size(0), -1)
     if table.dtype != torch.float32 or table.size(1) != HEAD_DIM or not table.is_contiguous() or table.device != device:
         raise ValueError(f"cos_sin_cache must be contiguous fp32 [max_position, {HEAD_DIM}] on the query device")
@@ -232,6 +233,9 @@ def qk_norm_rope_store(
                 raise ValueError("caches must be contiguous [pages, page, num_kv_heads, 128] in the query dtype")
         if slot_mapping.dtype not in (torch.int32, torch.int64) or slot_mapping.numel() != num_tokens:
             raise ValueError("slot_mapping must be int32/int64 with one slot per token")
+        if slot_mapping.device != device:
+            raise ValueError("slot_mapping must be on the query device")
+        slot_mapping = slot_mapping.reshape(-1).contiguous()
     if num_tokens == 0:
         return q_out, k_out
     _native.call(
@@ -307,6 +311,7 @@ def store_kvcache(
         raise TypeError("key and value dtypes differ")
     if not key.is_cuda or not slot_mapping.is_cuda or slot_mapping.device != key.device:
         raise RuntimeError("store_kvcache expects CUDA tensors on one device")
+    slot_mapping = slot_mapping.reshape(-1).contiguous()  # the kernel indexes it densely
     if num_tokens == 0:
         return
     _native.call(
@@ -390,6 +395,9 @@ def paged_decode(
     ``merges`` (see :func:`decode_merge_list`) lists the split segments whose
     partials the follow-up merge kernel combines.
     """
+    _check_paged(q, out, k_cache, v_cache,
+                 (("block_tables", block_tables), ("seq_lens", seq_lens), ("items", items),
+                  ("merges", merges), ("wave_extra", wave_extra)), (("workspace", workspace),))
     num_q_heads, head_dim = q.shape[1], q.shape[2]
     num_pages, page_size, num_kv_heads = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
     ws_ptr = workspace.data_ptr() if workspace is not None else 0
@@ -440,6 +448,9 @@ def paged_decode_store(
     :func:`decode_store_error`).  ``key``/``value`` are ``[T, Hkv, D]`` with
     unit inner stride; ``slot_mapping`` int32/int64 ``[T]`` (``< 0`` = skip).
     """
+    _check_paged(q, out, k_cache, v_cache,
+                 (("block_tables", block_tables), ("seq_lens", seq_lens), ("items", items),
+                  ("merges", merges), ("wave_extra", wave_extra)), (("workspace", workspace),))
     num_q_heads, head_dim = q.shape[1], q.shape[2]
     num_pages, page_size, num_kv_heads = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
     num_tokens = key.shape[0]
@@ -456,6 +467,7 @@ def paged_decode_store(
         raise ValueError("key and value need unit stride in the last dimension")
     if slot_mapping.numel() != num_tokens or slot_mapping.dtype not in (torch.int32, torch.int64):
         raise ValueError("slot_mapping must be int32/int64 with one slot per token")
+    slot_mapping = slot_mapping.reshape(-1).contiguous()  # the kernel indexes it densely
     ws_ptr = workspace.data_ptr() if workspace is not None else 0
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _native.call(
@@ -502,6 +514,9 @@ def paged_decode_graph(
     """
     if min(counts.numel(), 3) != 3 or wave_extra.numel() < 2:
         raise ValueError("graph decode needs 3 counts and at least one wavefront")
+    _check_paged(q, out, k_cache, v_cache,
+                 (("block_tables", block_tables), ("seq_lens", seq_lens), ("counts", counts), ("items", items),
+                  ("wave_extra", wave_extra), ("merges", merges)), (("workspace", workspace),))
     num_q_heads, head_dim = q.shape[1], q.shape[2]
     num_pages, page_size, num_kv_heads = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
     _native.call(
@@ -517,6 +532,35 @@ def paged_decode_graph(
         num_q_heads, num_kv_heads, head_dim, page_size, float(softmax_scale),
         _native.dtype_code(q.dtype), _native.stream_handle(q.device),
     )
+
+
+def _check_paged(q, out, k_cache, v_cache, int32_arrays=(), buffers=()) -> None:
+    """The checks the C ABI cannot make: every pointer it gets is device memory
+    on the query's GPU, the metadata arrays are int32 and dense (the block
+    table's rows may be strided: its row stride crosses the ABI), and the V
+    cache has the K cache's shape and strides (only the K strides cross the
+    ABI).  Shapes, alignment and head counts are checked there."""
+    device = q.device
+    if not q.is_cuda:
+        raise RuntimeError("paged attention expects CUDA tensors")
+    for name, t in (("out", out), ("k_cache", k_cache), ("v_cache", v_cache)):
+        if t.device != device:
+            raise RuntimeError(f"paged attention: {name} must be on the query's device")
+        if t.dtype != q.dtype:
+            raise TypeError(f"paged attention: {name} must have the query dtype")
+    if v_cache.shape != k_cache.shape or v_cache.stride() != k_cache.stride() or k_cache.dim() != 4:
+        raise ValueError("paged attention: k_cache and v_cache must be [pages, page, Hkv, D] of one layout")
+    if k_cache.stride(3) != 1 or k_cache.stride(2) != k_cache.size(3):
+        raise ValueError("paged attention: cache rows must be packed heads of unit-stride elements")
+    for name, t in int32_arrays:
+        if t is None:
+            continue
+        dense = t.stride(-1) == 1 if name == "block_tables" else t.is_contiguous()
+        if t.device != device or t.dtype != torch.int32 or not dense:
+            raise ValueError(f"paged attention: {name} must be a dense int32 CUDA tensor on the query's device")
+    for name, t in buffers:
+        if t is not None and (t.device != device or not t.is_contiguous()):
+            raise ValueError(f"paged attention: {name} must be a contiguous CUDA tensor on the query's device")
 
 
 def _paged_args(q, k_cache, v_cache, block_tables, seq_lens):
@@ -584,6 +628,9 @@ def paged_prefill(
     ``prefill_workspace_bytes(max_tiles)`` bytes); ``max_tiles`` must bound
     the tile count (see :func:`prefill_max_tiles`).
     """
+    _check_paged(q, out, k_cache, v_cache,
+                 (("block_tables", block_tables), ("seq_lens", seq_lens), ("query_start_loc", query_start_loc)),
+                 (("workspace", workspace),))
     _native.call(
         "mva_paged_prefill",
         *_paged_args(q, k_cache, v_cache, block_tables, seq_lens),
@@ -619,6 +666,9 @@ def paged_mixed(
     inside the launch (no merge list).  ``workspace`` is the decode
     workspace.
     """
+    _check_paged(q, out, k_cache, v_cache,
+                 (("block_tables", block_tables), ("seq_lens", seq_lens), ("query_start_loc", query_start_loc),
+                  ("decode_items", decode_items)), (("workspace", workspace),))
     _native.call(
         "mva_paged_mixed",
         *_paged_args(q, k_cache, v_cache, block_tables, seq_lens),

@@ -248,3 +248,31 @@ def test_one_backend_replans_many_steps_through_its_staging_ring(gpu):
     torch.cuda.synchronize()
     for batch, out in steps:
         assert_attention_close(out, _expected(batch))
+
+
+def test_raw_op_rejects_foreign_and_mistyped_tensors(gpu):
+    """The raw op refuses, before any launch, the tensors the C ABI cannot
+    check: host metadata, int64 metadata, and a V cache laid out unlike K."""
+    batch = make_paged_batch(62, [1, 1], [40, 17], 0, 16, 8)
+    common, q, kc, vc = _to(batch, gpu)
+    counts = np.asarray([3, 2])
+    items, nw, slots = make_decode_plan(counts, 0, 0, 8, 4, 1, 1)
+    ws = torch.zeros(ops.decode_workspace_bytes(slots, 8, 2), dtype=torch.uint8, device=gpu)
+    out = torch.zeros_like(q)
+    merges = ops.decode_merge_list(items)
+    good = dict(q=q, k_cache=kc, v_cache=vc, block_tables=common.block_tables, seq_lens=common.seq_lens,
+                items=_to_device(items, gpu), num_items=items.shape[0], num_waves=nw,
+                merges=_to_device(merges, gpu), num_merges=merges.shape[0], num_part_slots=slots, out=out,
+                workspace=ws, softmax_scale=128 ** -0.5)
+    bad = [
+        {"seq_lens": common.seq_lens.cpu()},
+        {"block_tables": common.block_tables.to(torch.int64)},
+        {"items": _to_device(items, gpu).t().contiguous().t()},
+        {"v_cache": vc.transpose(0, 1).contiguous().transpose(0, 1)},
+        {"out": out.to(torch.float16)},
+    ]
+    for change in bad:
+        with pytest.raises((ValueError, TypeError, RuntimeError)):
+            ops.paged_decode(**{**good, **change})
+    ops.paged_decode(**good)
+    assert_attention_close(out, _expected(batch))

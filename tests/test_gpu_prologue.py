@@ -96,3 +96,59 @@ def test_rotary_embedding_custom_op(gpu):
     out_q, _ = rope_op.forward_fused(pos.to(gpu), qd, kd, None, qn, kn, None, None, None)
     exp_q, _ = qk_norm_rope(*_views(qkv, 16, 8)[:2], pos, table, qn.weight.cpu(), kn.weight.cpu(), 1e-6)
     assert (out_q.cpu().float() - exp_q.float()).abs().max().item() <= 2 ** -5
+
+
+@pytest.mark.parametrize("tokens,hq,hkv,slot_dtype", [
+    (9, 12, 3, torch.int64),      # 18 rows per token: the last quad holds two
+    (33, 64, 8, torch.int32),     # 80 rows: four chunks per token
+    (41, 16, 8, torch.int64),
+    (9000, 32, 8, torch.int32),   # 18,000 chunks: the wavefronts loop past the grid cap
+])
+def test_prologue_store_shapes_and_slot_types(gpu, tokens, hq, hkv, slot_dtype):
+    """RoPE + store without norms: q, k and both cache rows bit-exact for
+    int32 and int64 slot mappings; slots of -1 or past the cache are
+    skipped and their rows left untouched."""
+    qkv, pos = _packed(tokens, hq, hkv, 25)
+    table = rope_cos_sin_cache(128, 4096, 1e6)
+    q, k, v = _views(qkv, hq, hkv)
+    g = torch.Generator().manual_seed(26)
+    num_slots = ((tokens + 4 + 15) // 16) * 16
+    slots = torch.randperm(num_slots, generator=g)[:tokens].to(slot_dtype)
+    slots[::7] = -1
+    slots[3::11] = num_slots + 5  # past the cache: skipped, as the reference's callers never send
+    k_cache = torch.full((num_slots // 16, 16, hkv, 128), 7.0, dtype=torch.bfloat16, device=gpu)
+    v_cache = torch.full_like(k_cache, 7.0)
+    qd, kd, vd = _views(qkv.to(gpu), hq, hkv)
+    got_q, got_k = ops.qk_norm_rope_store(pos.to(gpu), qd, kd, table.to(gpu), None, None, 1e-6,
+                                          vd, k_cache, v_cache, slots.to(gpu))
+    exp_k = rope(k, pos, table)
+    assert torch.equal(got_q.cpu(), rope(q, pos, table)) and torch.equal(got_k.cpu(), exp_k)
+    kc, vc = k_cache.cpu().view(-1, hkv, 128), v_cache.cpu().view(-1, hkv, 128)
+    live = (slots >= 0) & (slots < num_slots)
+    idx = slots[live].long()
+    assert torch.equal(kc[idx], exp_k[live]) and torch.equal(vc[idx], v[live])
+    untouched = torch.ones(num_slots, dtype=torch.bool)
+    untouched[idx] = False
+    assert bool((kc[untouched] == 7.0).all()) and bool((vc[untouched] == 7.0).all())
+
+
+def test_prologue_strided_slot_mapping_and_host_slots(gpu):
+    """A strided slot_mapping view stores at the slots it shows; a host
+    slot_mapping is refused before any launch."""
+    tokens, hq, hkv = 12, 16, 8
+    qkv, pos = _packed(tokens, hq, hkv, 27)
+    table = rope_cos_sin_cache(128, 4096, 1e6)
+    _, k, v = _views(qkv, hq, hkv)
+    wide = torch.arange(2 * tokens, dtype=torch.int32).flip(0)  # slots 2T-1, ..., 0
+    slots = wide[::2]  # stride 2: 2T-1, 2T-3, ...
+    k_cache = torch.zeros((2, 16, hkv, 128), dtype=torch.bfloat16, device=gpu)
+    v_cache = torch.zeros_like(k_cache)
+    qd, kd, vd = _views(qkv.to(gpu), hq, hkv)
+    with pytest.raises(ValueError):
+        ops.qk_norm_rope_store(pos.to(gpu), qd, kd, table.to(gpu), None, None, 1e-6, vd, k_cache, v_cache, slots)
+    _, got_k = ops.qk_norm_rope_store(pos.to(gpu), qd, kd, table.to(gpu), None, None, 1e-6, vd, k_cache, v_cache,
+                                      wide.to(gpu)[::2])
+    kc, vc = k_cache.cpu().view(-1, hkv, 128), v_cache.cpu().view(-1, hkv, 128)
+    idx = slots.long()
+    assert torch.equal(kc[idx], rope(k, pos, table)) and torch.equal(vc[idx], v)
+    assert bool((kc[idx - 1] == 0).all())  # the even slots the view skips stay untouched
