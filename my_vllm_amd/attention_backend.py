@@ -342,8 +342,10 @@ class PinnedStaging:
         buf[: host.size].copy_(torch.from_numpy(host))
         out = torch.empty(host.size, dtype=torch.int32, device=device)
         out.copy_(buf[: host.size], non_blocking=True)
+        # The copy runs on `device`'s current stream, which need not be the
+        # current device's: record there.
         event = torch.cuda.Event()
-        event.record()
+        event.record(torch.cuda.current_stream(device))
         self._events[k] = event
         return out
 
@@ -986,7 +988,7 @@ class MI355XAttentionBackendMixin:
                                state.merge_capacity, staging.numpy())
         state.plan_buffer.copy_(staging, non_blocking=True)
         event = torch.cuda.Event()
-        event.record()
+        event.record(torch.cuda.current_stream(state.plan_buffer.device))
         state.staging_ready[k] = event
         bt = metadata.block_tables
         state.block_tables_buffer[:, : bt.size(1)].copy_(bt)
