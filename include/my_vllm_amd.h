@@ -185,6 +185,48 @@ int mva_paged_decode(const void* q, int64_t q_token_stride, int64_t q_head_strid
                      int page_size, float softmax_scale, int dtype, void* stream);
 
 /*
+ * Host-side planners of mva_paged_decode's pieces (no device memory, no HIP
+ * call; safe without a GPU).  Sequence first_seq + i has block_counts[i] > 0
+ * pages and reads query row first_q_row + i.  Both write items [*, 8] as
+ * mva_paged_decode takes them and, when `merges` is not NULL, the merge list
+ * (the chunk-0 piece of every split segment, in item order), and set
+ * out_counts[4] = {num_items, num_waves, num_part_slots, num_merges}.
+ * Replace the host scheduling of FlashInfer's
+ * BatchDecodeWithPagedKVCacheWrapper.plan, called per step by the
+ * reference's build_plan (nanovllm/layers/attention_backend.py:826-840,
+ * :877-889).
+ *
+ * Piece lists: the batch's pages, in batch order, cut into
+ * G = min(num_groups, total pages) near-equal ranges (range g = pages
+ * [g*T/G, (g+1)*T/G)); wavefront g*num_kv_heads + h streams KV head h of
+ * range g, one piece per sequence the range touches, cut further to at most
+ * max_piece_pages (1 .. 128).  wave_extra gets G*num_kv_heads + 1 entries
+ * (the mva_paged_decode argument).  item_rows must be at least
+ * mva_decode_plan_listed_rows(...), an upper bound on the rows written.
+ */
+int64_t mva_decode_plan_listed_rows(int64_t num_seqs, int64_t total_pages, int num_kv_heads, int num_groups,
+                                    int max_piece_pages);
+int mva_decode_plan_listed(const int64_t* block_counts, int64_t num_seqs, int64_t first_seq,
+                           int64_t first_q_row, int num_kv_heads, int num_groups, int max_piece_pages,
+                           int32_t* items, int64_t item_rows, int32_t* wave_extra, int64_t wave_extra_len,
+                           int32_t* merges, int64_t merge_rows, int64_t* out_counts);
+
+/*
+ * Claims: every (sequence, KV head) segment of L pages cut into
+ * ceil(L / P) near-equal pieces, P = clamp(ceil(total segment pages /
+ * max(1, num_waves * max(1, pieces_per_wave))), min_piece_pages,
+ * max_piece_pages); pieces longest first, then sequence-major with the KV
+ * head fastest.  num_waves of the result = min(num_waves, num_items) (at
+ * least 1).  item_rows must be at least mva_decode_plan_claims_rows(...).
+ */
+int64_t mva_decode_plan_claims_rows(int64_t num_seqs, int64_t total_pages, int num_kv_heads,
+                                    int min_piece_pages);
+int mva_decode_plan_claims(const int64_t* block_counts, int64_t num_seqs, int64_t first_seq,
+                           int64_t first_q_row, int num_kv_heads, int64_t num_waves, double pieces_per_wave,
+                           int min_piece_pages, int max_piece_pages, int32_t* items, int64_t item_rows,
+                           int32_t* merges, int64_t merge_rows, int64_t* out_counts);
+
+/*
  * mva_paged_decode with the slot_mapping KV store of the same step folded in
  * (piece lists only: wave_extra is required).  Before reading any page, the
  * wavefront whose piece holds the last page of a sequence writes the new

@@ -114,6 +114,25 @@ _SIGNATURES = {
             _i32, _i32, _i32, _i32, _f32, _i32, _c_void_p,  # heads, head_dim, page, scale, dtype, stream
         ],
     ),
+    "mva_decode_plan_listed_rows": (_i64, [_i64, _i64, _i32, _i32, _i32]),
+    "mva_decode_plan_listed": (
+        _i32,
+        [
+            _c_void_p, _i64, _i64, _i64,  # block_counts, num_seqs, first_seq, first_q_row
+            _i32, _i32, _i32,  # num_kv_heads, num_groups, max_piece_pages
+            _c_void_p, _i64, _c_void_p, _i64,  # items, item_rows, wave_extra, wave_extra_len
+            _c_void_p, _i64, _c_void_p,  # merges, merge_rows, out_counts
+        ],
+    ),
+    "mva_decode_plan_claims_rows": (_i64, [_i64, _i64, _i32, _i32]),
+    "mva_decode_plan_claims": (
+        _i32,
+        [
+            _c_void_p, _i64, _i64, _i64,  # block_counts, num_seqs, first_seq, first_q_row
+            _i32, _i64, ctypes.c_double, _i32, _i32,  # num_kv_heads, num_waves, pieces/wave, piece bounds
+            _c_void_p, _i64, _c_void_p, _i64, _c_void_p,  # items, item_rows, merges, merge_rows, out_counts
+        ],
+    ),
     "mva_prefill_tile_tokens": (_i32, [_i32, _i32]),
     "mva_prefill_workspace_bytes": (_i64, [_i64]),
     "mva_paged_prefill": (
@@ -144,7 +163,7 @@ _SIGNATURES = {
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 # The C ABI revision these signatures describe (mva_abi_version()).
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

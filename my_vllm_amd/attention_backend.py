@@ -124,6 +124,48 @@ def resident_decode_waves(device: torch.device | None = None, mixed: bool = Fals
     return 256 * per_cu
 
 
+def _plan_counts(block_counts) -> np.ndarray:
+    counts = np.ascontiguousarray(block_counts, dtype=np.int64).reshape(-1)
+    if np.any(counts <= 0):
+        raise ValueError("every decode sequence needs at least one page")
+    return counts
+
+
+def plan_decode_claims(
+    block_counts: np.ndarray | tuple[int, ...],
+    first_seq: int,
+    first_q_row: int,
+    num_kv_heads: int,
+    num_waves: int,
+    pieces_per_wave: float = 1.5,
+    min_piece_pages: int = 4,
+    max_piece_pages: int = ops.MAX_CHUNK_PAGES,
+) -> tuple[np.ndarray, int, int, np.ndarray]:
+    """:func:`make_decode_plan` plus its merge list (as
+    :func:`ops.decode_merge_list` would give it), from the library's native
+    planner ``mva_decode_plan_claims``."""
+    counts = _plan_counts(block_counts)
+    if not 1 <= min_piece_pages <= max_piece_pages <= ops.MAX_CHUNK_PAGES:
+        raise ValueError("piece length bounds must satisfy 1 <= min <= max <= 128")
+    n = counts.size
+    if n == 0:
+        empty = np.zeros((0, ops.DECODE_ITEM_INTS), np.int32)
+        return empty, 0, 0, empty
+    rows = int(_native.query("mva_decode_plan_claims_rows", n, int(counts.sum()), int(num_kv_heads),
+                             int(min_piece_pages)))
+    if rows < 0:
+        raise ValueError("invalid decode plan arguments")
+    items = np.empty((rows, ops.DECODE_ITEM_INTS), np.int32)
+    merges = np.empty((n * int(num_kv_heads), ops.DECODE_ITEM_INTS), np.int32)
+    out = np.zeros(4, np.int64)
+    _native.call("mva_decode_plan_claims", counts.ctypes.data, n, int(first_seq), int(first_q_row),
+                 int(num_kv_heads), int(num_waves), float(pieces_per_wave), int(min_piece_pages),
+                 int(max_piece_pages), items.ctypes.data, rows, merges.ctypes.data, merges.shape[0],
+                 out.ctypes.data)
+    num_items, waves, slots, num_merges = (int(x) for x in out)
+    return items[:num_items], waves, slots, merges[:num_merges]
+
+
 def make_decode_plan(
     block_counts: np.ndarray | tuple[int, ...],
     first_seq: int,
@@ -150,46 +192,11 @@ def make_decode_plan(
     first, then sequence-major with the KV head fastest (the head slices of
     one page are neighbours in the cache).  Returns ``(items, waves,
     num_part_slots)`` with ``waves = min(num_waves, len(items))``, the grid to
-    launch.
+    launch.  The plan is computed by the library's host-side planner
+    (``mva_decode_plan_claims``), once per step.
     """
-    counts = np.asarray(block_counts, dtype=np.int64)
-    if counts.size == 0:
-        return np.zeros((0, ops.DECODE_ITEM_INTS), np.int32), 0, 0
-    if np.any(counts <= 0):
-        raise ValueError("every decode sequence needs at least one page")
-    if not 1 <= min_piece_pages <= max_piece_pages <= ops.MAX_CHUNK_PAGES:
-        raise ValueError("piece length bounds must satisfy 1 <= min <= max <= 128")
-    seg_len = np.repeat(counts, num_kv_heads)
-    nseg = seg_len.size
-    total = int(seg_len.sum())
-    target = max(1, int(num_waves * max(1.0, float(pieces_per_wave))))
-    piece = int(np.clip(-(-total // target), min_piece_pages, max_piece_pages))
-    nchunks = (seg_len + piece - 1) // piece
-    seg_of = np.repeat(np.arange(nseg), nchunks)
-    first_piece = np.cumsum(nchunks) - nchunks
-    chunk = np.arange(int(nchunks.sum())) - np.repeat(first_piece, nchunks)
-    n_of = nchunks[seg_of]
-    len_of = seg_len[seg_of]
-    # Near-equal cut of L pages into n pieces: piece k covers [k*L//n, (k+1)*L//n).
-    begin = (chunk * len_of) // n_of
-    end = ((chunk + 1) * len_of) // n_of
-    # Every KV head of a sequence has the same length and so the same cut:
-    # partial slots are numbered per sequence.
-    seq_split = np.where(nchunks[::num_kv_heads] > 1, nchunks[::num_kv_heads], 0)
-    seq_base = np.cumsum(seq_split) - seq_split
-    items = np.zeros((seg_of.size, ops.DECODE_ITEM_INTS), dtype=np.int32)
-    items[:, 0] = first_seq + seg_of // num_kv_heads
-    items[:, 1] = begin
-    items[:, 2] = end
-    items[:, 3] = chunk
-    items[:, 4] = n_of
-    items[:, 5] = seq_base[seg_of // num_kv_heads]
-    items[:, 6] = first_q_row + seg_of // num_kv_heads
-    items[:, 7] = seg_of % num_kv_heads
-    order = np.argsort(-(end - begin), kind="stable")
-    items = items[order]
-    waves = max(1, min(int(num_waves), items.shape[0]))
-    return items, waves, int(seq_split.sum())
+    return plan_decode_claims(block_counts, first_seq, first_q_row, num_kv_heads, num_waves, pieces_per_wave,
+                              min_piece_pages, max_piece_pages)[:3]
 
 
 # Workgroups of a piece-list decode launch fill 8 wave slots per CU (the
@@ -225,6 +232,41 @@ def listed_decode_groups(num_kv_heads: int, device: torch.device | None = None) 
     return max(1, waves // num_kv_heads), per_group
 
 
+def plan_decode_listed(
+    block_counts: np.ndarray | tuple[int, ...],
+    first_seq: int,
+    first_q_row: int,
+    num_kv_heads: int,
+    num_groups: int,
+    max_piece_pages: int = ops.MAX_CHUNK_PAGES,
+) -> tuple[np.ndarray, np.ndarray, int, int, np.ndarray]:
+    """:func:`make_decode_plan_listed` plus its merge list (as
+    :func:`ops.decode_merge_list` would give it), from the library's native
+    planner ``mva_decode_plan_listed``."""
+    counts = _plan_counts(block_counts)
+    if not 1 <= max_piece_pages <= ops.MAX_CHUNK_PAGES:
+        raise ValueError("piece length must be in [1, 128] pages")
+    n = counts.size
+    if n == 0:
+        empty = np.zeros((0, ops.DECODE_ITEM_INTS), np.int32)
+        return empty, np.zeros(1, np.int32), 0, 0, empty
+    hkv = int(num_kv_heads)
+    total = int(counts.sum())
+    num_groups = max(1, int(num_groups))
+    rows = int(_native.query("mva_decode_plan_listed_rows", n, total, hkv, num_groups, int(max_piece_pages)))
+    if rows < 0:
+        raise ValueError("invalid decode plan arguments")
+    items = np.empty((rows, ops.DECODE_ITEM_INTS), np.int32)
+    merges = np.empty((n * hkv, ops.DECODE_ITEM_INTS), np.int32)
+    wave_extra = np.empty(min(num_groups, total) * hkv + 1, np.int32)
+    out = np.zeros(4, np.int64)
+    _native.call("mva_decode_plan_listed", counts.ctypes.data, n, int(first_seq), int(first_q_row), hkv,
+                 num_groups, int(max_piece_pages), items.ctypes.data, rows, wave_extra.ctypes.data,
+                 wave_extra.size, merges.ctypes.data, merges.shape[0], out.ctypes.data)
+    num_items, waves, slots, num_merges = (int(x) for x in out)
+    return items[:num_items], wave_extra, waves, slots, merges[:num_merges]
+
+
 def make_decode_plan_listed(
     block_counts: np.ndarray | tuple[int, ...],
     first_seq: int,
@@ -247,59 +289,11 @@ def make_decode_plan_listed(
 
     Returns ``(items, wave_extra, waves, num_part_slots)``: items hold the
     first piece of wavefront ``w`` at row ``w`` and its later pieces, in page
-    order, at rows ``wave_extra[w] .. wave_extra[w + 1] - 1``.
+    order, at rows ``wave_extra[w] .. wave_extra[w + 1] - 1``.  The plan is
+    computed by the library's host-side planner (``mva_decode_plan_listed``),
+    once per step.
     """
-    counts = np.asarray(block_counts, dtype=np.int64)
-    if counts.size == 0:
-        return np.zeros((0, ops.DECODE_ITEM_INTS), np.int32), np.zeros(1, np.int32), 0, 0
-    if np.any(counts <= 0):
-        raise ValueError("every decode sequence needs at least one page")
-    if not 1 <= max_piece_pages <= ops.MAX_CHUNK_PAGES:
-        raise ValueError("piece length must be in [1, 128] pages")
-    hkv = int(num_kv_heads)
-    offsets = np.concatenate(([0], np.cumsum(counts)))
-    total = int(offsets[-1])
-    groups = max(1, min(int(num_groups), total))
-    bounds = (np.arange(groups + 1, dtype=np.int64) * total) // groups
-    # Breakpoints of both partitions: every interval lies in one range and
-    # one sequence.
-    cuts = np.union1d(bounds, offsets)
-    starts, ends = cuts[:-1], cuts[1:]
-    group_of = np.searchsorted(bounds, starts, side="right") - 1
-    seq_of = np.searchsorted(offsets, starts, side="right") - 1
-    lengths = ends - starts
-    ncut = (lengths + max_piece_pages - 1) // max_piece_pages
-    iv = np.repeat(np.arange(starts.size), ncut)
-    k = np.arange(iv.size) - np.repeat(np.cumsum(ncut) - ncut, ncut)
-    p_begin = starts[iv] + (k * lengths[iv]) // ncut[iv]
-    p_end = starts[iv] + ((k + 1) * lengths[iv]) // ncut[iv]
-    piece_group = group_of[iv]
-    piece_seq = seq_of[iv]
-    per_seq = np.bincount(piece_seq, minlength=counts.size)
-    chunk = np.arange(iv.size) - (np.cumsum(per_seq) - per_seq)[piece_seq]
-    split = np.where(per_seq > 1, per_seq, 0)
-    part_base = np.cumsum(split) - split
-    pieces = np.zeros((iv.size, hkv, ops.DECODE_ITEM_INTS), dtype=np.int32)
-    pieces[:, :, 0] = (first_seq + piece_seq)[:, None]
-    pieces[:, :, 1] = (p_begin - offsets[piece_seq])[:, None]
-    pieces[:, :, 2] = (p_end - offsets[piece_seq])[:, None]
-    pieces[:, :, 3] = chunk[:, None]
-    pieces[:, :, 4] = per_seq[piece_seq][:, None]
-    pieces[:, :, 5] = part_base[piece_seq][:, None]
-    pieces[:, :, 6] = (first_q_row + piece_seq)[:, None]
-    pieces[:, :, 7] = np.arange(hkv)[None, :]
-    wave_of = (piece_group[:, None] * hkv + np.arange(hkv)[None, :]).reshape(-1)
-    pieces = pieces.reshape(-1, ops.DECODE_ITEM_INTS)
-    order = np.argsort(wave_of, kind="stable")  # page order within a wavefront
-    pieces, wave_of = pieces[order], wave_of[order]
-    waves = groups * hkv
-    per_wave = np.bincount(wave_of, minlength=waves)
-    first = np.cumsum(per_wave) - per_wave
-    is_first = np.zeros(pieces.shape[0], dtype=bool)
-    is_first[first] = True
-    items = np.concatenate([pieces[first], pieces[~is_first]])
-    wave_extra = waves + np.concatenate(([0], np.cumsum(per_wave - 1)))
-    return items, wave_extra.astype(np.int32), waves, int(split.sum())
+    return plan_decode_listed(block_counts, first_seq, first_q_row, num_kv_heads, num_groups, max_piece_pages)[:4]
 
 
 def _to_device(array: np.ndarray, device: torch.device) -> torch.Tensor:
@@ -562,11 +556,16 @@ class MI355XAttentionBackendMixin:
                 raise TypeError("trusted block_counts must be a tuple")
             if len(block_counts) != common.num_seqs:
                 raise ValueError("trusted block_counts length must equal num_seqs")
-            if any(
-                isinstance(count, bool) or not isinstance(count, int) or not 0 < count <= max_pages
-                for count in block_counts
+            # Plain ints within range (the common case) pass on two builtin
+            # scans; anything else is judged element by element.
+            if not all(type(count) is int for count in block_counts) or (
+                block_counts and not (min(block_counts) > 0 and max(block_counts) <= max_pages)
             ):
-                raise ValueError("trusted block_counts contains an invalid row count")
+                if any(
+                    isinstance(count, bool) or not isinstance(count, int) or not 0 < count <= max_pages
+                    for count in block_counts
+                ):
+                    raise ValueError("trusted block_counts contains an invalid row count")
             counts = np.asarray(block_counts, dtype=np.int64)
         else:
             page_counts = (common.seq_lens.to(torch.int64) + self.block_size - 1) // self.block_size
@@ -601,7 +600,7 @@ class MI355XAttentionBackendMixin:
             decode_counts = counts[common.num_prefill_seqs:]
             wave_extra = None
             if one_launch:
-                items, num_decode_waves, num_part_slots = make_decode_plan(
+                items, num_decode_waves, num_part_slots, _ = plan_decode_claims(
                     decode_counts, common.num_prefill_seqs, common.num_prefill_tokens, self.num_kv_heads,
                     resident_decode_waves(block_tables.device, mixed=True),
                 )
@@ -612,19 +611,20 @@ class MI355XAttentionBackendMixin:
             if not one_launch:
                 if decode_schedule(int(decode_counts.sum()), self.num_kv_heads) == "listed":
                     groups, waves_per_group = listed_decode_groups(self.num_kv_heads, block_tables.device)
-                    items, wave_extra, num_decode_waves, num_part_slots = make_decode_plan_listed(
+                    items, wave_extra, num_decode_waves, num_part_slots, merges = plan_decode_listed(
                         decode_counts, common.num_prefill_seqs, common.num_prefill_tokens, self.num_kv_heads, groups
                     )
                 else:
-                    items, num_decode_waves, num_part_slots = make_decode_plan(
+                    items, num_decode_waves, num_part_slots, merges = plan_decode_claims(
                         decode_counts,
                         common.num_prefill_seqs,
                         common.num_prefill_tokens,
                         self.num_kv_heads,
                         resident_decode_waves(block_tables.device),
                     )
-            # The single MIXED launch merges split segments itself.
-            merges = np.zeros((0, ops.DECODE_ITEM_INTS), np.int32) if one_launch else ops.decode_merge_list(items)
+            else:
+                # The single MIXED launch merges split segments itself.
+                merges = np.zeros((0, ops.DECODE_ITEM_INTS), np.int32)
             num_decode_items = items.shape[0]
             num_decode_merges = merges.shape[0]
             # Pieces, merge entries and piece-list offsets share one
@@ -652,7 +652,7 @@ class MI355XAttentionBackendMixin:
             query_start_loc=common.query_start_loc,
             seq_lens=common.seq_lens,
             block_tables=block_tables,
-            kv_indptr=tuple(int(x) for x in offsets),
+            kv_indptr=tuple(offsets.tolist()),
             num_pages=num_pages,
             num_prefill_pages=num_prefill_pages,
             decode_items=decode_items,
@@ -973,8 +973,7 @@ class MI355XAttentionBackendMixin:
         host = metadata.decode_host_plan
         if host is None or host[3] != state.groups:
             counts = np.diff(np.asarray(metadata.kv_indptr, dtype=np.int64))
-            items, wave_extra, _, _ = make_decode_plan_listed(counts, 0, 0, self.num_kv_heads, state.groups)
-            merges = ops.decode_merge_list(items)
+            items, wave_extra, _, _, merges = plan_decode_listed(counts, 0, 0, self.num_kv_heads, state.groups)
         else:
             items, wave_extra, merges, _ = host
         # Staging buffers alternate: the one refilled now was last copied two
@@ -1140,5 +1139,7 @@ __all__ = [
     "integrate",
     "make_decode_plan",
     "make_decode_plan_listed",
+    "plan_decode_claims",
+    "plan_decode_listed",
     "resident_decode_waves",
 ]
