@@ -256,7 +256,7 @@ def cpu_baseline(batch, seconds: float):
 def extra_measurements(device, steps: int):
     from my_vllm_amd import ops
     from my_vllm_amd.attention_backend import MI355XAttentionBackend
-    from workloads import config_long_decode, config_mixed, config_prefill, silu_input
+    from workloads import config_decode_small, config_long_decode, config_mixed, config_prefill, silu_input
 
     res = {}
     # SiLU-and-mul, Qwen3-0.6B MLP: 8 rotating inputs (600 MB > Infinity Cache).
@@ -321,6 +321,7 @@ def extra_measurements(device, steps: int):
     res["mixed_unified_ms"] = round(ms_u, 4)
     res["mixed_split_ms"] = round(ms_s, 4)
     res["mixed_unified_roofline_frac"] = round(bound_ms / ms_u, 4)
+    res.update(host_planning(device, [("mixed_budget8192", batch, 32, 8)]))
     del batch
 
     # Context for the MFMA-bound figures: the vendor library's dense bf16 GEMM
@@ -334,6 +335,7 @@ def extra_measurements(device, steps: int):
     del ga, gb
 
     res.update(graph_vs_eager(device))
+    res.update(host_planning(device, [("decode_64seq", config_decode_small(seed=1), 16, 8)]))
 
     # Long-context decode, Qwen3-32B (one layer's KV, ~10.7 GB).
     batch = config_long_decode(seed=4, device=device, rng_device="cuda")
@@ -391,6 +393,28 @@ def prologue_fused_vs_separate(device, tokens: int = 4096, hq: int = 32, hkv: in
     return {"prologue_4096tok_fused_us": round(fused_ms * 1e3, 2),
             "prologue_4096tok_separate_us": round(sep_ms * 1e3, 2),
             "prologue_4096tok_fused_GBps": round(moved / fused_ms / 1e6, 1)}
+
+
+def host_planning(device, cases, reps: int = 200):
+    """Host time of one step's planning (``build_plan``: metadata checks, the
+    decode planner, the pinned staging copy) per ``(name, batch, hq, hkv)``
+    case, trusted metadata as the engine passes it; the copies are left in
+    flight, as in a serving loop."""
+    from my_vllm_amd.attention_backend import MI355XAttentionBackend
+
+    res = {}
+    for name, batch, hq, hkv in cases:
+        backend = MI355XAttentionBackend(hq, hkv, 128, 16, torch.bfloat16)
+        common = to_device(batch, device)
+        for _ in range(10):
+            backend.build_plan(common)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            backend.build_plan(common)
+        res[f"build_plan_{name}_host_us"] = round((time.perf_counter() - t0) / reps * 1e6, 1)
+        torch.cuda.synchronize()
+    return res
 
 
 def graph_vs_eager(device, batch_size: int = 8, ctx: int = 512, steps: int = 200):

@@ -861,7 +861,7 @@ class MI355XAttentionBackendMixin:
                 metadata.decode_items, metadata.num_decode_items, metadata.num_decode_waves,
                 metadata.decode_merges, metadata.num_decode_merges, metadata.num_decode_part_slots,
                 output, workspace, self.softmax_scale,
-                metadata.decode_wave_extra, metadata.decode_waves_per_group,
+                metadata.decode_wave_extra, metadata.decode_waves_per_group, validate=False,
             )
             return
         ops.paged_decode(
@@ -881,6 +881,7 @@ class MI355XAttentionBackendMixin:
             self.softmax_scale,
             metadata.decode_wave_extra,
             metadata.decode_waves_per_group,
+            validate=False,
         )
 
     def fused_store_error(self) -> bool:
@@ -895,7 +896,7 @@ class MI355XAttentionBackendMixin:
         ops.paged_decode_graph(
             q, k_cache, v_cache, state.block_tables_buffer, state.seq_lens_buffer, counts, items, wave_extra,
             state.waves_per_group, merges, state.part_slot_capacity, state.output, state.workspace,
-            self.softmax_scale,
+            self.softmax_scale, validate=False,
         )
 
     # ---- full-decode HIP graph (reference attention_backend.py:242-275, 1028-1225) ----

@@ -203,7 +203,8 @@ def qk_norm_rope_store(
         raise ValueError("positions must be int64 [tokens] and key must have the query's token count")
     if positions.device != device:
         raise ValueError("positions must be on the query device")
-    positions = positions.contiguous()  # the kernel indexes it densely
+    if not positions.is_contiguous():
+        positions = positions.contiguous()  # the kernel indexes it densely
     table = cos_sin_cache.reshape(cos_sin_cache.size(0), -1)
     if table.dtype != torch.float32 or table.size(1) != HEAD_DIM or not table.is_contiguous() or table.device != device:
         raise ValueError(f"cos_sin_cache must be contiguous fp32 [max_position, {HEAD_DIM}] on the query device")
@@ -235,7 +236,8 @@ def qk_norm_rope_store(
             raise ValueError("slot_mapping must be int32/int64 with one slot per token")
         if slot_mapping.device != device:
             raise ValueError("slot_mapping must be on the query device")
-        slot_mapping = slot_mapping.reshape(-1).contiguous()
+        if slot_mapping.dim() != 1 or not slot_mapping.is_contiguous():
+            slot_mapping = slot_mapping.reshape(-1).contiguous()  # the kernel indexes it densely
     if num_tokens == 0:
         return q_out, k_out
     _native.call(
@@ -311,7 +313,8 @@ def store_kvcache(
         raise TypeError("key and value dtypes differ")
     if not key.is_cuda or not slot_mapping.is_cuda or slot_mapping.device != key.device:
         raise RuntimeError("store_kvcache expects CUDA tensors on one device")
-    slot_mapping = slot_mapping.reshape(-1).contiguous()  # the kernel indexes it densely
+    if slot_mapping.dim() != 1 or not slot_mapping.is_contiguous():
+        slot_mapping = slot_mapping.reshape(-1).contiguous()  # the kernel indexes it densely
     if num_tokens == 0:
         return
     _native.call(
@@ -383,6 +386,8 @@ def paged_decode(
     softmax_scale: float,
     wave_extra: torch.Tensor | None = None,
     waves_per_group: int = 1,
+    *,
+    validate: bool = True,
 ) -> None:
     """Launch the paged GQA decode kernel over prepared pieces.
 
@@ -395,9 +400,10 @@ def paged_decode(
     ``merges`` (see :func:`decode_merge_list`) lists the split segments whose
     partials the follow-up merge kernel combines.
     """
-    _check_paged(q, out, k_cache, v_cache,
-                 (("block_tables", block_tables), ("seq_lens", seq_lens), ("items", items),
-                  ("merges", merges), ("wave_extra", wave_extra)), (("workspace", workspace),))
+    if validate:
+        _check_paged(q, out, k_cache, v_cache,
+                     (("block_tables", block_tables), ("seq_lens", seq_lens), ("items", items),
+                      ("merges", merges), ("wave_extra", wave_extra)), (("workspace", workspace),))
     num_q_heads, head_dim = q.shape[1], q.shape[2]
     num_pages, page_size, num_kv_heads = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
     ws_ptr = workspace.data_ptr() if workspace is not None else 0
@@ -437,6 +443,8 @@ def paged_decode_store(
     softmax_scale: float,
     wave_extra: torch.Tensor,
     waves_per_group: int = 1,
+    *,
+    validate: bool = True,
 ) -> None:
     """:func:`store_kvcache` of this step's ``key``/``value`` and :func:`paged_decode`
     in one launch (piece lists only).
@@ -448,9 +456,10 @@ def paged_decode_store(
     :func:`decode_store_error`).  ``key``/``value`` are ``[T, Hkv, D]`` with
     unit inner stride; ``slot_mapping`` int32/int64 ``[T]`` (``< 0`` = skip).
     """
-    _check_paged(q, out, k_cache, v_cache,
-                 (("block_tables", block_tables), ("seq_lens", seq_lens), ("items", items),
-                  ("merges", merges), ("wave_extra", wave_extra)), (("workspace", workspace),))
+    if validate:
+        _check_paged(q, out, k_cache, v_cache,
+                     (("block_tables", block_tables), ("seq_lens", seq_lens), ("items", items),
+                      ("merges", merges), ("wave_extra", wave_extra)), (("workspace", workspace),))
     num_q_heads, head_dim = q.shape[1], q.shape[2]
     num_pages, page_size, num_kv_heads = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
     num_tokens = key.shape[0]
@@ -467,7 +476,8 @@ def paged_decode_store(
         raise ValueError("key and value need unit stride in the last dimension")
     if slot_mapping.numel() != num_tokens or slot_mapping.dtype not in (torch.int32, torch.int64):
         raise ValueError("slot_mapping must be int32/int64 with one slot per token")
-    slot_mapping = slot_mapping.reshape(-1).contiguous()  # the kernel indexes it densely
+    if slot_mapping.dim() != 1 or not slot_mapping.is_contiguous():
+        slot_mapping = slot_mapping.reshape(-1).contiguous()  # the kernel indexes it densely
     ws_ptr = workspace.data_ptr() if workspace is not None else 0
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _native.call(
@@ -503,6 +513,8 @@ def paged_decode_graph(
     out: torch.Tensor,
     workspace: torch.Tensor,
     softmax_scale: float,
+    *,
+    validate: bool = True,
 ) -> None:
     """Fixed-shape decode launch for HIP graph capture.
 
@@ -514,9 +526,10 @@ def paged_decode_graph(
     """
     if min(counts.numel(), 3) != 3 or wave_extra.numel() < 2:
         raise ValueError("graph decode needs 3 counts and at least one wavefront")
-    _check_paged(q, out, k_cache, v_cache,
-                 (("block_tables", block_tables), ("seq_lens", seq_lens), ("counts", counts), ("items", items),
-                  ("wave_extra", wave_extra), ("merges", merges)), (("workspace", workspace),))
+    if validate:
+        _check_paged(q, out, k_cache, v_cache,
+                     (("block_tables", block_tables), ("seq_lens", seq_lens), ("counts", counts), ("items", items),
+                      ("wave_extra", wave_extra), ("merges", merges)), (("workspace", workspace),))
     num_q_heads, head_dim = q.shape[1], q.shape[2]
     num_pages, page_size, num_kv_heads = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
     _native.call(
@@ -539,7 +552,11 @@ def _check_paged(q, out, k_cache, v_cache, int32_arrays=(), buffers=()) -> None:
     on the query's GPU, the metadata arrays are int32 and dense (the block
     table's rows may be strided: its row stride crosses the ABI), and the V
     cache has the K cache's shape and strides (only the K strides cross the
-    ABI).  Shapes, alignment and head counts are checked there."""
+    ABI).  Shapes, alignment and head counts are checked there.  The attention
+    backend, which checks the query and caches itself on every forward and
+    builds the work lists, calls the ops with ``validate=False``: on a
+    launch-bound decode step these checks are a visible share of the host
+    time."""
     device = q.device
     if not q.is_cuda:
         raise RuntimeError("paged attention expects CUDA tensors")
@@ -620,6 +637,8 @@ def paged_prefill(
     workspace: torch.Tensor,
     out: torch.Tensor,
     softmax_scale: float,
+    *,
+    validate: bool = True,
 ) -> None:
     """Launch the ragged causal prefill over the first ``num_seqs`` sequences.
 
@@ -628,9 +647,10 @@ def paged_prefill(
     ``prefill_workspace_bytes(max_tiles)`` bytes); ``max_tiles`` must bound
     the tile count (see :func:`prefill_max_tiles`).
     """
-    _check_paged(q, out, k_cache, v_cache,
-                 (("block_tables", block_tables), ("seq_lens", seq_lens), ("query_start_loc", query_start_loc)),
-                 (("workspace", workspace),))
+    if validate:
+        _check_paged(q, out, k_cache, v_cache,
+                     (("block_tables", block_tables), ("seq_lens", seq_lens), ("query_start_loc", query_start_loc)),
+                     (("workspace", workspace),))
     _native.call(
         "mva_paged_prefill",
         *_paged_args(q, k_cache, v_cache, block_tables, seq_lens),
@@ -657,6 +677,8 @@ def paged_mixed(
     out: torch.Tensor,
     workspace: torch.Tensor,
     softmax_scale: float,
+    *,
+    validate: bool = True,
 ) -> None:
     """One launch: prefill tiles write ``out[:P]``, decode pieces write ``out[P:]``.
 
@@ -666,9 +688,10 @@ def paged_mixed(
     inside the launch (no merge list).  ``workspace`` is the decode
     workspace.
     """
-    _check_paged(q, out, k_cache, v_cache,
-                 (("block_tables", block_tables), ("seq_lens", seq_lens), ("query_start_loc", query_start_loc),
-                  ("decode_items", decode_items)), (("workspace", workspace),))
+    if validate:
+        _check_paged(q, out, k_cache, v_cache,
+                     (("block_tables", block_tables), ("seq_lens", seq_lens), ("query_start_loc", query_start_loc),
+                      ("decode_items", decode_items)), (("workspace", workspace),))
     _native.call(
         "mva_paged_mixed",
         *_paged_args(q, k_cache, v_cache, block_tables, seq_lens),
