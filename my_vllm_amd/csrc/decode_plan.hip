@@ -145,6 +145,8 @@ extern "C" int mva_decode_plan_listed(const int64_t* block_counts, int64_t num_s
   }
   const int64_t np = (int64_t)pieces.size();
   if (np * hkv > item_rows) return set_error("decode plan: item capacity too small");
+  if (np * hkv > std::numeric_limits<int32_t>::max())  // wave_extra holds int32 row indices
+    return set_error("decode plan: more than 2^31-1 pieces");
 
   // Chunk numbers in page order, and the partial slots of split sequences.
   std::vector<int64_t> per_seq((size_t)num_seqs, 0), part_base((size_t)num_seqs, 0), chunk((size_t)np);
@@ -154,6 +156,7 @@ extern "C" int mva_decode_plan_listed(const int64_t* block_counts, int64_t num_s
     part_base[(size_t)q] = slots;
     if (per_seq[(size_t)q] > 1) slots += per_seq[(size_t)q];
   }
+  if (slots > std::numeric_limits<int32_t>::max()) return set_error("decode plan: more than 2^31-1 partial slots");
 
   // Wavefront w = g * Hkv + h streams head h of range g's pieces: its first
   // piece at row w, the rest (page order) at rows wave_extra[w] ..
@@ -229,6 +232,7 @@ extern "C" int mva_decode_plan_claims(const int64_t* block_counts, int64_t num_s
     rows += n * hkv;
   }
   if (rows > item_rows) return set_error("decode plan: item capacity too small");
+  if (slots > std::numeric_limits<int32_t>::max()) return set_error("decode plan: more than 2^31-1 partial slots");
   // Row where each length's pieces start, longest first.
   std::vector<int64_t> next((size_t)kMaxPiecePages + 2, 0);
   int64_t at = 0;
