@@ -123,16 +123,17 @@ int mva_qk_norm_rope_store(const void* q_in, void* q_out, int64_t q_token_stride
 /*
  * Bytes of device workspace mva_paged_decode / mva_paged_mixed need for
  * `num_part_slots` split-K partial slots (a scheduler area of piece-claim
- * counters, then fp32 partial outputs and log-sum-exps), or -1 for invalid
- * arguments.  The workspace must be zeroed once when first allocated; the
- * kernels leave the counters zeroed again on return.  Launches that share a
+ * counters, MIXED arrival counters and fused-store row flags, then fp32
+ * partial outputs and log-sum-exps), or -1 for invalid arguments.  The
+ * workspace must be zeroed once when first allocated; the kernels leave the
+ * counters and flags zeroed again on return.  Launches that share a
  * workspace must not overlap.
  */
 int64_t mva_decode_workspace_bytes(int64_t num_part_slots, int num_kv_heads, int group);
 
 /* Byte offset, inside a decode workspace, of the int32 word that
- * mva_paged_decode_store sets when a new row's slot is not in its sequence's
- * last page. */
+ * mva_paged_decode_store sets when a new row's slot is not its sequence's
+ * last position. */
 #define MVA_DECODE_STORE_ERROR_OFFSET 4224
 
 /*
@@ -233,12 +234,16 @@ int mva_decode_plan_claims(const int64_t* block_counts, int64_t num_seqs, int64_
  * K and V rows of that piece's KV head, k_new / v_new
  * [num_new_tokens, num_kv_heads, 128] (row q_row of the piece, any 4-byte
  * aligned strides), to cache slot slot_mapping[q_row] (int32, or int64 when
- * slot_is_int64; -1 skips).  The slot must lie in the sequence's last page,
- * as the model runner builds it; then the output and the caches equal
- * mva_kv_store followed by mva_paged_decode.  A row whose slot lies in any
- * other page is not written (another wavefront may be reading that page):
- * the launch sets the int32 word at byte MVA_DECODE_STORE_ERROR_OFFSET of the
- * workspace to 1, and only the caller clears it.  Other arguments as
+ * slot_is_int64; -1 skips) when that slot is the sequence's last position
+ * (last page, row (seq_len - 1) % 16), as the model runner builds it; then
+ * the output and the caches equal mva_kv_store followed by
+ * mva_paged_decode.  Every other row t < num_new_tokens with a slot >= 0 (a
+ * slot elsewhere, which another wavefront may be reading, or a row no piece
+ * names) is written by the merge kernel that always follows on the stream,
+ * after the attention read the cache: the caches always equal
+ * mva_kv_store's, and the launch sets the int32 word at byte
+ * MVA_DECODE_STORE_ERROR_OFFSET of the workspace to 1 (only the caller
+ * clears it).  num_new_tokens * num_kv_heads <= 65536.  Other arguments as
  * mva_paged_decode.
  * Replaces the KVCacheStore call (nanovllm/layers/attention.py:140-141)
  * together with the decode run that follows it (attention_backend.py:995-997).
@@ -330,6 +335,11 @@ int mva_prefill_tile_tokens(int num_q_heads, int num_kv_heads);
  * max_tiles query tiles, or -1 for an invalid count. */
 int64_t mva_prefill_workspace_bytes(int64_t max_tiles);
 
+/* Byte offset, inside a prefill workspace, of the int32 word where
+ * mva_paged_prefill writes how many of the batch's tiles exceeded max_tiles
+ * (and were not run). */
+#define MVA_PREFILL_DROPPED_TILES_OFFSET 4
+
 /*
  * Ragged causal chunked prefill over prefix-cached pages (same cache and q/out
  * conventions as mva_paged_decode).  Sequence s < num_seqs has query rows
@@ -343,7 +353,10 @@ int64_t mva_prefill_workspace_bytes(int64_t max_tiles);
  * (mva_prefill_workspace_bytes(max_tiles) bytes, 16-byte aligned).
  * max_tiles must bound the tile count, e.g. num_prefill_tokens / tile_tokens
  * + num_seqs with tile_tokens = 2 * mva_prefill_tile_tokens(); tiles beyond
- * it are not run.  A sequence with no queries, or more queries than keys, is
+ * it are not run (their output rows keep what `out` held), and the launch
+ * writes their number to the int32 word at byte
+ * MVA_PREFILL_DROPPED_TILES_OFFSET of the workspace (0 when max_tiles bounds
+ * the batch).  A sequence with no queries, or more queries than keys, is
  * skipped.  A persistent grid of 512-thread workgroups, one per CU, then
  * streams the tiles.  Launches that share a workspace must not overlap.
  * Replaces FlashInfer BatchPrefillWithPagedKVCacheWrapper.plan/run on the

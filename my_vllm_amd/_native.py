@@ -163,7 +163,7 @@ _SIGNATURES = {
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 # The C ABI revision these signatures describe (mva_abi_version()).
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

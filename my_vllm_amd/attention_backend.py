@@ -21,7 +21,6 @@ backend-owned output buffer:
 
 from __future__ import annotations
 
-import os
 from dataclasses import dataclass
 from types import MappingProxyType
 from typing import Any
@@ -91,12 +90,14 @@ class MI355XAttentionMetadata:
     # Host copy of a piece-list plan: (items, wave_extra, merges, workgroups).
     decode_host_plan: tuple | None = None
     # Bounds on the prefill query tiles (size the device-built tile list and
-    # the MIXED launch's prefill pool).  mixed_prefill_max_tiles == 0 on a
-    # MIXED_UNIFIED plan: more prefill sequences, KV heads or split-K
-    # segments than one MIXED launch takes, so the batch runs as prefill +
-    # decode launches.
+    # the MIXED launch's prefill pool).  On a MIXED batch,
+    # mixed_prefill_max_tiles > 0 means one launch; 0 means prefill +
+    # decode launches, for the reason in mixed_split_reason (split mode, or
+    # more prefill sequences, KV heads or split-K pairs than one MIXED
+    # launch takes).
     prefill_max_tiles: int = 0
     mixed_prefill_max_tiles: int = 0
+    mixed_split_reason: str | None = None
 
     @property
     def is_cacheless(self) -> bool:
@@ -113,9 +114,11 @@ _DECODE_WAVES_PER_CU = 5
 _MIXED_DECODE_WAVES_PER_CU = 6
 
 
-def resident_decode_waves(device: torch.device | None = None, mixed: bool = False) -> int:
-    """Decode wavefronts per launch: CUs x 5 (x 6 in a MIXED launch); 1280 / 1536 on MI355X."""
-    override = os.environ.get("MVA_DECODE_WAVES")
+def resident_decode_waves(device: torch.device | None = None, mixed: bool = False,
+                          override: int | None = None) -> int:
+    """Decode wavefronts per launch: CUs x 5 (x 6 in a MIXED launch); 1280 / 1536 on MI355X.
+
+    ``override`` (a backend's ``decode_waves_override``) replaces the count."""
     if override:
         return max(1, int(override))
     per_cu = _MIXED_DECODE_WAVES_PER_CU if mixed else _DECODE_WAVES_PER_CU
@@ -208,26 +211,30 @@ _LISTED_WAVES_PER_CU = 8
 _LISTED_MAX_BYTES = 2 << 30
 
 
-def decode_schedule(total_pages: int, num_kv_heads: int, elem_bytes: int = 2) -> str:
-    """"listed" or "claims" for a decode batch of ``total_pages`` pages."""
-    forced = os.environ.get("MVA_DECODE_SCHEDULE")
-    if forced in ("listed", "claims"):
+def decode_schedule(total_pages: int, num_kv_heads: int, elem_bytes: int = 2, forced: str | None = None) -> str:
+    """"listed" or "claims" for a decode batch of ``total_pages`` pages (``forced``,
+    a backend's ``decode_schedule_override``, picks one)."""
+    if forced is not None:
+        if forced not in ("listed", "claims"):
+            raise ValueError("decode schedule must be 'listed' or 'claims'")
         return forced
     kv_bytes = total_pages * PAGE_SIZE * num_kv_heads * HEAD_DIM * elem_bytes * 2
     return "listed" if kv_bytes <= _LISTED_MAX_BYTES else "claims"
 
 
-def listed_decode_groups(num_kv_heads: int, device: torch.device | None = None) -> tuple[int, int]:
+def listed_decode_groups(num_kv_heads: int, device: torch.device | None = None,
+                         override: int | None = None) -> tuple[int, int]:
     """(workgroups, wavefronts per workgroup) of a piece-list decode launch.
 
     A workgroup holds one wavefront per KV head when the head count divides 8
     (so one CU streams every head of the same pages), else one wavefront.
+    ``override`` (a backend's ``decode_waves_override``) sets the wavefront
+    count the workgroups share.
     """
     per_group = num_kv_heads if num_kv_heads in (1, 2, 4, 8) else 1
     cus = 256
     if device is not None and device.type == "cuda":
         cus = torch.cuda.get_device_properties(device).multi_processor_count
-    override = os.environ.get("MVA_DECODE_WAVES")
     waves = max(1, int(override)) if override else cus * _LISTED_WAVES_PER_CU
     return max(1, waves // num_kv_heads), per_group
 
@@ -449,6 +456,15 @@ class MI355XAttentionBackendMixin:
     # Metadata tensors must live on the GPU (the reference's contract,
     # attention_backend.py:1436-1440); host-only planning tests relax it.
     require_device_metadata = True
+    # Planning overrides, set as attributes by tests and tuning scripts (never
+    # read from the environment): the decode wavefront count, and "listed" or
+    # "claims" for the decode schedule.  None keeps the measured defaults.
+    decode_waves_override: int | None = None
+    decode_schedule_override: str | None = None
+    # Debug check of forward_with_kv_store: read the fused store's error word
+    # after each fused launch (a device read) and raise if a row's slot was
+    # not its sequence's last position.
+    check_fused_store: bool = False
 
     def __init__(
         self,
@@ -474,6 +490,7 @@ class MI355XAttentionBackendMixin:
         _native.load_library()
         self.attention_mode = attention_mode
         self._reset_state()
+        self._mixed_attention_unavailable_reason = self._backend_mixed_reason()
 
     def _reset_state(self) -> None:
         self._planned_route: str | None = None
@@ -536,6 +553,41 @@ class MI355XAttentionBackendMixin:
     def route_counts(self):
         return MappingProxyType(dict(self._route_counts))
 
+    # ---- MIXED capability (reference attention_backend.py:626-663) -----------
+    @property
+    def mixed_attention_available(self) -> bool:
+        """Whether MIXED batches run as one launch (route MIXED_UNIFIED).
+
+        False in split mode and beyond one MIXED launch's limits; after a
+        MIXED batch is planned it describes that batch, so the route
+        ``build_plan`` returned always equals the capability route
+        (``"mixed_unified"`` if available, else ``"mixed_split"``).
+        """
+        return self._mixed_attention_unavailable_reason is None
+
+    @property
+    def mixed_attention_unavailable_reason(self) -> str | None:
+        """Why MIXED batches run as prefill + decode launches (None when they
+        run as one launch)."""
+        return self._mixed_attention_unavailable_reason
+
+    def _backend_mixed_reason(self) -> str | None:
+        if self.attention_mode != "unified":
+            return "unified mixed attention is disabled in split mode"
+        if self.num_kv_heads > ops.MIXED_MAX_KV_HEADS:
+            return (f"one MIXED launch takes at most {ops.MIXED_MAX_KV_HEADS} KV heads, "
+                    f"the backend has {self.num_kv_heads}")
+        return None
+
+    def _batch_mixed_reason(self, common) -> str | None:
+        """Why this MIXED batch cannot run as one launch (None if it can),
+        before its decode plan is known."""
+        reason = self._backend_mixed_reason()
+        if reason is None and common.num_prefill_seqs > ops.MIXED_PREFILL_SEQS_MAX:
+            reason = (f"one MIXED launch orders at most {ops.MIXED_PREFILL_SEQS_MAX} prefill sequences, "
+                      f"the batch has {common.num_prefill_seqs}")
+        return reason
+
     # ---- per-step metadata and plan ------------------------------------------
     def build_metadata(self, common) -> MI355XAttentionMetadata:
         check_common_metadata(common, require_cuda=self.require_device_metadata, common_type=self.common_type)
@@ -594,23 +646,32 @@ class MI355XAttentionBackendMixin:
         num_decode_waves = 0
         num_part_slots = 0
         waves_per_group = 1
-        # A MIXED batch runs as one launch when it fits that launch's limits.
-        one_launch = bool(common.num_prefill_seqs and common.num_decode_seqs) and self._mixed_in_one_launch(common)
+        # A MIXED batch runs as one launch when it fits that launch's limits;
+        # split_reason says why not.
+        mixed = bool(common.num_prefill_seqs and common.num_decode_seqs)
+        split_reason = self._batch_mixed_reason(common) if mixed else None
+        one_launch = mixed and split_reason is None
         if common.num_decode_seqs:
             decode_counts = counts[common.num_prefill_seqs:]
             wave_extra = None
             if one_launch:
                 items, num_decode_waves, num_part_slots, _ = plan_decode_claims(
                     decode_counts, common.num_prefill_seqs, common.num_prefill_tokens, self.num_kv_heads,
-                    resident_decode_waves(block_tables.device, mixed=True),
+                    resident_decode_waves(block_tables.device, mixed=True, override=self.decode_waves_override),
                 )
                 # Its split-K arrival counters cover a bounded number of
                 # (partial slot, KV head) pairs.
                 if num_part_slots * self.num_kv_heads > ops.MIXED_ARRIVAL_COUNTERS:
                     one_launch = False
+                    split_reason = (f"one MIXED launch merges at most {ops.MIXED_ARRIVAL_COUNTERS} split-K "
+                                    f"(partial slot, KV head) pairs, the decode plan has "
+                                    f"{num_part_slots * self.num_kv_heads}")
             if not one_launch:
-                if decode_schedule(int(decode_counts.sum()), self.num_kv_heads) == "listed":
-                    groups, waves_per_group = listed_decode_groups(self.num_kv_heads, block_tables.device)
+                schedule = decode_schedule(int(decode_counts.sum()), self.num_kv_heads,
+                                           forced=self.decode_schedule_override)
+                if schedule == "listed":
+                    groups, waves_per_group = listed_decode_groups(self.num_kv_heads, block_tables.device,
+                                                                   override=self.decode_waves_override)
                     items, wave_extra, num_decode_waves, num_part_slots, merges = plan_decode_listed(
                         decode_counts, common.num_prefill_seqs, common.num_prefill_tokens, self.num_kv_heads, groups
                     )
@@ -620,7 +681,7 @@ class MI355XAttentionBackendMixin:
                         common.num_prefill_seqs,
                         common.num_prefill_tokens,
                         self.num_kv_heads,
-                        resident_decode_waves(block_tables.device),
+                        resident_decode_waves(block_tables.device, override=self.decode_waves_override),
                     )
             else:
                 # The single MIXED launch merges split segments itself.
@@ -666,15 +727,7 @@ class MI355XAttentionBackendMixin:
             decode_host_plan=decode_host_plan,
             prefill_max_tiles=prefill_max_tiles,
             mixed_prefill_max_tiles=mixed_prefill_max_tiles,
-        )
-
-    def _mixed_in_one_launch(self, common) -> bool:
-        """Unified mode runs a MIXED batch as one launch within that launch's
-        limits (prefill sequences, KV heads), else as prefill + decode."""
-        return (
-            self.attention_mode == "unified"
-            and common.num_prefill_seqs <= ops.MIXED_PREFILL_SEQS_MAX
-            and self.num_kv_heads <= ops.MIXED_MAX_KV_HEADS
+            mixed_split_reason=split_reason if mixed and not one_launch else None,
         )
 
     def build_plan(self, common, metadata: MI355XAttentionMetadata | None = None):
@@ -692,10 +745,15 @@ class MI355XAttentionBackendMixin:
             route = Route.PREFILL
         elif batch_type is Batch.PURE_DECODE:
             route = Route.DECODE
-        elif self.attention_mode == "unified":
-            route = Route.MIXED_UNIFIED
         else:
-            route = Route.MIXED_SPLIT
+            # MIXED_UNIFIED exactly when the metadata plans one launch; the
+            # capability properties then describe this batch.
+            one_launch = metadata.mixed_prefill_max_tiles > 0
+            route = Route.MIXED_UNIFIED if one_launch else Route.MIXED_SPLIT
+            self._mixed_attention_unavailable_reason = (
+                None if one_launch else metadata.mixed_split_reason or self._backend_mixed_reason()
+                or "the MIXED metadata was planned for prefill + decode launches"
+            )
         plan = self.plan_type(batch_type, route, common, metadata)
         self._planned_route = route.value
         self._route_counts[route.value] += 1
@@ -757,12 +815,17 @@ class MI355XAttentionBackendMixin:
         """The KV store of ``Attention.forward`` (``attention.py:140-141``) followed by
         :meth:`forward`, as one call.
 
-        A DECODE step of trusted metadata (the model runner's, whose slots
-        lie in each sequence's last page) planned with piece lists writes the
-        new rows inside the decode launch (``mva_paged_decode_store``): the
-        result and the caches are those of the store followed by the decode.
-        Every other step runs ``store`` (the layer's ``KVCacheStore``; the
-        HIP store when None) and then :meth:`forward`.
+        A DECODE step of trusted metadata planned with piece lists writes the
+        new rows inside the decode launch (``mva_paged_decode_store``).  The
+        model runner's slots are each sequence's last position
+        (``model_runner.py:361-484``); for those the result and the caches
+        are those of the store followed by the decode.  A row with any other
+        slot is still written (by the kernel after the decode), so the caches
+        always match the store, but this step's attention did not see it
+        there; the workspace error word records it (``fused_store_error``,
+        or ``check_fused_store`` to raise at once).  Every other step runs
+        ``store`` (the layer's ``KVCacheStore``; the HIP store when None) and
+        then :meth:`forward`.
         """
         metadata = plan.metadata if isinstance(plan, self.plan_type) else None
         if (
@@ -777,12 +840,17 @@ class MI355XAttentionBackendMixin:
             and v is not None
             and k.dim() == 3
             and k.size(0) == q.size(0)
+            and k.size(0) * self.num_kv_heads <= ops.FUSED_STORE_MAX_ROWS
         ):
             self._pending_store = (k, v, slot_mapping)
             try:
-                return self.forward(q, k, v, k_cache, v_cache, plan)
+                out = self.forward(q, k, v, k_cache, v_cache, plan)
             finally:
                 self._pending_store = None
+            if self.check_fused_store and self.fused_store_error():
+                raise RuntimeError("fused KV store: a new row's slot is not its sequence's last position; "
+                                   "the cache holds the row, but this step's attention did not see it there")
+            return out
         (store if store is not None else ops.store_kvcache)(k, v, k_cache, v_cache, slot_mapping)
         return self.forward(q, k, v, k_cache, v_cache, plan)
 
@@ -824,6 +892,10 @@ class MI355XAttentionBackendMixin:
             raise RuntimeError(f"invalid planned MI355X route: {route!r}")
         if plan.batch_type is not expected:
             raise ValueError("MI355X route does not match the planned BatchType")
+        # The metadata fixes how a MIXED batch runs: a single launch's decode
+        # plan has no merge list, a split plan's has.
+        if expected is Batch.MIXED and (route is Route.MIXED_UNIFIED) != (metadata.mixed_prefill_max_tiles > 0):
+            raise ValueError("MI355X MIXED route does not match the planned metadata")
         if not has_k_cache:
             raise ValueError("paged MI355X route requires an allocated KV cache")
         if metadata.is_cacheless:
@@ -840,7 +912,7 @@ class MI355XAttentionBackendMixin:
         if route is Route.PREFILL:
             self._run_prefill(q, k_cache, v_cache, common, metadata, output)
             return output
-        if route is Route.MIXED_SPLIT or metadata.mixed_prefill_max_tiles == 0:
+        if route is Route.MIXED_SPLIT:
             if common.num_prefill_seqs:
                 self._run_prefill(q, k_cache, v_cache, common, metadata, output)
             if common.num_decode_seqs:
@@ -885,8 +957,9 @@ class MI355XAttentionBackendMixin:
         )
 
     def fused_store_error(self) -> bool:
-        """Whether a folded decode store since the last call skipped a row
-        whose slot was not in its sequence's last page (reads the device)."""
+        """Whether a folded decode store since the last call met a row whose
+        slot was not its sequence's last position (written after the
+        attention; reads the device and clears the word)."""
         if self._workspace is None:
             return False
         return ops.decode_store_error(self._workspace)
@@ -910,7 +983,8 @@ class MI355XAttentionBackendMixin:
         graph_device = torch.device(device)
         if graph_device.type != "cuda":
             raise ValueError("full decode graph state must be on CUDA")
-        groups, waves_per_group = listed_decode_groups(self.num_kv_heads, graph_device)
+        groups, waves_per_group = listed_decode_groups(self.num_kv_heads, graph_device,
+                                                       override=self.decode_waves_override)
         caps = graph_decode_capacities(batch_size, page_indices_capacity, self.num_kv_heads, groups)
         group = self.num_q_heads // self.num_kv_heads
         plan_ints = graph_plan_buffer_ints(caps["item_capacity"], caps["wave_capacity"], caps["merge_capacity"])

@@ -231,6 +231,8 @@ extern "C" int mva_decode_plan_claims(const int64_t* block_counts, int64_t num_s
     for (int64_t k = 0; k < n; ++k) by_len[(size_t)((k + 1) * len / n - k * len / n)] += hkv;
     rows += n * hkv;
   }
+  // Pieces are claimed by int32 index on the device.
+  if (rows > std::numeric_limits<int32_t>::max()) return set_error("decode plan: more than 2^31-1 pieces");
   if (rows > item_rows) return set_error("decode plan: item capacity too small");
   if (slots > std::numeric_limits<int32_t>::max()) return set_error("decode plan: more than 2^31-1 partial slots");
   // Row where each length's pieces start, longest first.

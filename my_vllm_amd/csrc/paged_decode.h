@@ -95,7 +95,11 @@ struct DecodeParams {
   // Fused slot_mapping store (piece lists), or k_new == nullptr: before its
   // first page, a wavefront writes the new K/V row of (token q_row, KV head)
   // to cache slot slots[q_row] for every piece of its list that holds the
-  // sequence's last page (that piece is the only reader of the row).
+  // sequence's last page (that piece is the only reader of the row), when
+  // the slot is the sequence's last position, and sets
+  // store_flags[q_row * Hkv + kv_head].  The launch after it (the merge
+  // kernel) writes every row of [0, num_new) with a slot >= 0 whose flag is
+  // clear, and clears the flags.
   const void* k_new;
   int64_t kn_tok_stride;
   int64_t kn_head_stride;
@@ -105,6 +109,7 @@ struct DecodeParams {
   const void* slots;
   int slots_int64;
   int num_new;  // rows of k_new / v_new / slots
+  int32_t* store_flags;  // [kStoreFlagInts], zero between launches
   void* out;
   int64_t out_tok_stride;
   int64_t out_head_stride;
@@ -299,6 +304,10 @@ static_assert((kMixedPrefillCtrInt + kMixedPrefillMaxHeads * kDecodeSchedLineInt
 // (and partial layouts) used the workspace in between.
 constexpr int kArrivalCounters = 65536;
 constexpr int64_t kArrivalBytes = (int64_t)kArrivalCounters * 4;
+// Fused-store row flags: one int per (new row, KV head), in a fixed region
+// after the arrival counters; a fused launch takes at most this many pairs.
+constexpr int kStoreFlagInts = 65536;
+constexpr int64_t kStoreFlagBytes = (int64_t)kStoreFlagInts * 4;
 
 template <typename T, bool kAgent>
 __device__ void merge_segment(const DecodeParams& p, const i32x8& d, int g);
@@ -412,12 +421,14 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds, int* p
       if (d[6] < 0 || d[6] >= p.num_new || len <= 0 || d[1] * kPageSize >= len || d[2] * kPageSize < len) continue;
       const int64_t slot = p.slots_int64 ? ((const int64_t*)p.slots)[d[6]] : ((const int32_t*)p.slots)[d[6]];
       if (slot < 0) continue;  // -1: nothing to store
-      // The row must land in the sequence's last page, which this piece
-      // alone reads; a slot anywhere else could be a page another wavefront
-      // is streaming.  Such a row is not written, and the launch records it
-      // in the workspace's store-error word.
+      // The row must be the sequence's last position, in the last page,
+      // which this piece alone reads; a slot anywhere else could be in a
+      // page another wavefront is streaming.  Such a row is left to the
+      // merge kernel that follows (it writes every unflagged row), and the
+      // launch records it in the workspace's store-error word.
       const int last_page = sload(p.block_tables, (int64_t)d[0] * p.bt_stride + (len - 1) / kPageSize);
-      if (slot / kPageSize != last_page || slot / kPageSize >= p.num_pages) {
+      if (slot != (int64_t)last_page * kPageSize + (len - 1) % kPageSize || last_page < 0 ||
+          last_page >= p.num_pages) {
         if (lane == 0) *(volatile int32_t*)(p.sched + kDecodeStoreErrorInt) = 1;
         continue;
       }
@@ -429,6 +440,7 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds, int* p
                                             (int64_t)d[7] * p.vn_head_stride + 2 * lane);
       *(uint32_t*)((T*)const_cast<void*>(p.k_cache) + dst) = kv;
       *(uint32_t*)((T*)const_cast<void*>(p.v_cache) + dst) = vv;
+      if (lane == 0) p.store_flags[(int64_t)d[6] * p.num_kv_heads + d[7]] = 1;
     }
   }
   __builtin_amdgcn_s_waitcnt(kVmcnt0);
@@ -509,6 +521,16 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds, int* p
   // arrives last merges the segment with agent-scope loads and clears the
   // counter.  Arrivals at exit keep atomics out of the page stream; a
   // 65th split piece flushes the list first.
+  //
+  // Visibility rests on the ISA, not on release/acquire atomics: every
+  // partial store is an agent-scope write-through store (sc1, inline asm,
+  // so the compiler cannot move or merge it), s_waitcnt vmcnt(0) retires
+  // them -- written to memory -- before the arrival atomic issues, and the
+  // last arrival reads the partials with agent-scope loads, which do not
+  // hit in a non-coherent cache.  The memory model's agent-scope release
+  // and acquire would add an L2 write-back and an L2 invalidate per
+  // arrival, which measured 1.05 -> 1.16 ms on the budget-8192 MIXED batch
+  // (the invalidates evict the prefill tiles' K/V lines).
   int split_list = 0;
   int nsplit = 0;
   auto settle = [&]() __attribute__((always_inline)) {
@@ -818,6 +840,34 @@ __device__ void merge_segment(const DecodeParams& p, const i32x8& d, int g) {
   T* op = (T*)p.out + qrow * p.out_tok_stride + (int64_t)(h * G + g) * p.out_head_stride + 2 * lane;
   op[0] = (T)(a0 * winv);
   op[1] = (T)(a1 * winv);
+}
+
+// Late rows of a fused-store launch: wavefront `row` writes the K/V rows of
+// new token `row` (every KV head) that the decode launch did not write (flag
+// clear) to slot slots[row] -- as the separate store would, a slot < 0 or
+// past the cache is skipped -- and clears the row's flags.
+template <typename T>
+__device__ void decode_late_store_wave(const DecodeParams& p, int64_t row) {
+  const int lane = threadIdx.x & 63;
+  const int64_t slot = p.slots_int64 ? ((const int64_t*)p.slots)[row] : ((const int32_t*)p.slots)[row];
+  const bool ok = slot >= 0 && slot / kPageSize < p.num_pages;
+  for (int h = 0; h < p.num_kv_heads; ++h) {
+    int32_t* flag = p.store_flags + row * p.num_kv_heads + h;
+    const int32_t written = *flag;
+    if (written) {
+      if (lane == 0) *flag = 0;
+      continue;
+    }
+    if (!ok) continue;
+    const int64_t dst = (slot / kPageSize) * p.page_stride + (slot % kPageSize) * p.tok_stride +
+                        (int64_t)h * kHeadDim + 2 * lane;
+    const uint32_t kv = *(const uint32_t*)((const T*)p.k_new + row * p.kn_tok_stride +
+                                          (int64_t)h * p.kn_head_stride + 2 * lane);
+    const uint32_t vv = *(const uint32_t*)((const T*)p.v_new + row * p.vn_tok_stride +
+                                          (int64_t)h * p.vn_head_stride + 2 * lane);
+    *(uint32_t*)((T*)const_cast<void*>(p.k_cache) + dst) = kv;
+    *(uint32_t*)((T*)const_cast<void*>(p.v_cache) + dst) = vv;
+  }
 }
 
 // Split-K merge of one (split segment, query head g) of the merge list:

@@ -38,12 +38,20 @@ int launch_paged_decode(const DecodeParams& p, int waves_per_group, hipStream_t 
 }
 
 // Split-K merges: four wavefronts per workgroup, one per (merge entry,
-// query head).  Graph launches size the grid for the merge capacity and read
-// this step's merge count from p.counts[2].
+// query head), in the first merge_blocks workgroups.  Graph launches size the
+// grid for the merge capacity and read this step's merge count from
+// p.counts[2].  After a fused-store launch the workgroups past merge_blocks
+// write the late rows, one wavefront per new token.
 template <typename T>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, const int32_t* __restrict__ merges,
-                                                           int64_t num_waves) {
-  const int64_t v = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+                                                           int64_t num_waves, int64_t merge_blocks) {
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if ((int64_t)blockIdx.x >= merge_blocks) {
+    const int64_t row = ((int64_t)blockIdx.x - merge_blocks) * 4 + w;
+    if (row < p.num_new) decode_late_store_wave<T>(p, row);
+    return;
+  }
+  const int64_t v = (int64_t)blockIdx.x * 4 + w;
   if (v >= num_waves) return;
   if (p.counts != nullptr && v >= (int64_t)max(sload(p.counts, 2), 0) * p.group) return;
   decode_merge_wave<T>(p, merges, v);
@@ -52,26 +60,33 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, const
 }  // namespace
 
 // Launches the split-K merge kernel after a decode (or MIXED) launch on the
-// same stream; `merges` lists the split segments (piece descriptors).
+// same stream; `merges` lists the split segments (piece descriptors).  After
+// a fused-store launch (p.k_new set) it always runs: its late-store
+// workgroups write the new rows the decode launch left.
 int launch_decode_merge(const DecodeParams& p, const int32_t* merges, int64_t num_merges, int dtype,
                         hipStream_t stream) {
-  if (num_merges == 0) return 0;
+  const int64_t late_rows = p.k_new != nullptr ? p.num_new : 0;
+  if (num_merges == 0 && late_rows == 0) return 0;
   const int64_t waves = num_merges * p.group;
-  const int64_t blocks = (waves + 3) / 4;
+  const int64_t merge_blocks = (waves + 3) / 4;
+  const int64_t blocks = merge_blocks + (late_rows + 3) / 4;
   if (blocks > 0x7fffffffLL) return set_error("paged attention: too many split-K merges");
   if (dtype == kBF16)
-    hipLaunchKernelGGL(decode_merge_kernel<__bf16>, dim3((uint32_t)blocks), dim3(256), 0, stream, p, merges, waves);
+    hipLaunchKernelGGL(decode_merge_kernel<__bf16>, dim3((uint32_t)blocks), dim3(256), 0, stream, p, merges, waves,
+                       merge_blocks);
   else
-    hipLaunchKernelGGL(decode_merge_kernel<_Float16>, dim3((uint32_t)blocks), dim3(256), 0, stream, p, merges, waves);
+    hipLaunchKernelGGL(decode_merge_kernel<_Float16>, dim3((uint32_t)blocks), dim3(256), 0, stream, p, merges,
+                       waves, merge_blocks);
   return check_launch("decode_merge");
 }
 
 static int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
 // Workspace layout: [scheduler (kDecodeSchedBytes)][arrival counters
-// (kArrivalBytes, MIXED launches)][lse f32 slots*Hkv*G][o f32 slots*Hkv*G*D].
+// (kArrivalBytes, MIXED launches)][fused-store row flags (kStoreFlagBytes)]
+// [lse f32 slots*Hkv*G][o f32 slots*Hkv*G*D].
 int64_t decode_workspace_bytes(int64_t slots, int hkv, int group) {
-  return kDecodeSchedBytes + kArrivalBytes + align256(slots * hkv * group * 4) +
+  return kDecodeSchedBytes + kArrivalBytes + kStoreFlagBytes + align256(slots * hkv * group * 4) +
          align256(slots * hkv * group * kHeadDim * 4);
 }
 
@@ -137,6 +152,8 @@ int fill_decode_params(DecodeParams& p, const void* q, int64_t q_token_stride, i
   p.num_new = 0;
   p.sched = (int32_t*)ws;
   ws += kDecodeSchedBytes + kArrivalBytes;
+  p.store_flags = (int32_t*)ws;
+  ws += kStoreFlagBytes;
   p.part_lse = (float*)ws;
   ws += align256(num_part_slots * num_kv_heads * group * 4);
   p.part_o = (float*)ws;
@@ -204,6 +221,8 @@ extern "C" int mva_paged_decode_store(const void* q, int64_t q_token_stride, int
   if (k_new == nullptr || v_new == nullptr || slot_mapping == nullptr)
     return set_error("paged attention: the fused store needs k, v and slot_mapping");
   if (num_new_tokens < 0 || num_new_tokens > 0x7fffffffLL) return set_error("paged attention: invalid token count");
+  if (num_kv_heads > 0 && num_new_tokens * num_kv_heads > kStoreFlagInts)
+    return set_error("paged attention: the fused store takes at most 65536 (token, KV head) rows");
   if (((uint64_t)(uintptr_t)k_new | (uint64_t)(uintptr_t)v_new | (uint64_t)(k_token_stride * 2) |
        (uint64_t)(k_head_stride * 2) | (uint64_t)(v_token_stride * 2) | (uint64_t)(v_head_stride * 2)) % 4)
     return set_error("paged attention: k / v rows must be 4-byte aligned");
@@ -214,7 +233,6 @@ extern "C" int mva_paged_decode_store(const void* q, int64_t q_token_stride, int
                               out_token_stride, out_head_stride, workspace, workspace_bytes, num_q_heads,
                               num_kv_heads, head_dim, page_size, softmax_scale);
   if (rc) return rc;
-  if (num_items == 0) return 0;
   p.k_new = k_new;
   p.kn_tok_stride = k_token_stride;
   p.kn_head_stride = k_head_stride;
@@ -225,10 +243,13 @@ extern "C" int mva_paged_decode_store(const void* q, int64_t q_token_stride, int
   p.slots_int64 = slot_is_int64 ? 1 : 0;
   p.num_new = (int)num_new_tokens;
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == kBF16) rc = launch_paged_decode<__bf16>(p, waves_per_group, s);
-  else if (dtype == kF16) rc = launch_paged_decode<_Float16>(p, waves_per_group, s);
-  else return set_error("paged attention: dtype must be bf16 or fp16");
-  if (rc) return rc;
+  if (dtype != kBF16 && dtype != kF16) return set_error("paged attention: dtype must be bf16 or fp16");
+  // With no pieces every new row is a late row of the merge kernel.
+  if (num_items > 0) {
+    rc = dtype == kBF16 ? launch_paged_decode<__bf16>(p, waves_per_group, s)
+                        : launch_paged_decode<_Float16>(p, waves_per_group, s);
+    if (rc) return rc;
+  }
   return launch_decode_merge(p, merges, num_merges, dtype, s);
 }
 

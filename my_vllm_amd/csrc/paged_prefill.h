@@ -428,8 +428,11 @@ __device__ __attribute__((always_inline)) inline void prefill_core(const Prefill
 // causal bound.  Page ids past npages repeat the last page; ids outside the
 // cache read as page 0.
 constexpr int kPrefillPlanItemInts = 16;
-// Header: word 0 = tile count; the claim counter of KV head h at word
+// Header: word 0 = tile count (at most the capacity); word 1 = tiles of the
+// batch beyond the capacity, which are not run (0 when the capacity bounds
+// the batch); the claim counter of KV head h at word
 // kPrefillPlanLineInts * (1 + h), each on its own 128-byte line.
+constexpr int kPrefillPlanDroppedInt = 1;
 constexpr int kPrefillPlanLineInts = 32;
 constexpr int kPrefillPlanMaxHeads = 127;
 constexpr int kPrefillPlanHeaderInts = kPrefillPlanLineInts * (1 + kPrefillPlanMaxHeads);

@@ -28,7 +28,8 @@ namespace {
 // sequence's tiles largest key count first, so the tiles that read one
 // sequence's pages run together and long work starts early.  A sequence
 // with no queries, or with more queries than keys, gets no tile.  At most
-// `capacity` tiles are written; word 0 receives their number.
+// `capacity` tiles are written; word 0 receives their number and word 1
+// the number left out.
 __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* __restrict__ qsl,
                                                             const int32_t* __restrict__ seq_lens,
                                                             const int32_t* __restrict__ block_tables,
@@ -125,7 +126,10 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* __res
     }
     __syncthreads();
   }
-  if (tid == 0) plan[0] = min(carry, capacity);
+  if (tid == 0) {
+    plan[0] = min(carry, capacity);
+    plan[kPrefillPlanDroppedInt] = max(carry - capacity, 0);
+  }
   if (tid < num_kv_heads) plan[kPrefillPlanLineInts * (1 + tid)] = 0;  // claim counters
 }
 

@@ -35,7 +35,9 @@ def _lowered_copy(overrides: Mapping[str, str]) -> Mapping[str, str]:
 
 @dataclass(frozen=True)
 class CustomOpConfig:
-    """Construction-time platform and implementation choices for ordinary ops."""
+    """Which device family an operator binds to, and which provider each
+    operator name asks for (``overrides``: op name -> provider name, "auto"
+    when absent).  Immutable and hashable once built."""
 
     platform: str = "auto"
     dtype: torch.dtype | None = None
@@ -62,7 +64,9 @@ def default_platform() -> str:
 
 
 class CustomOp(nn.Module):
-    """Platform-dispatched base class for ordinary operators."""
+    """An operator module whose ``forward`` is chosen once, when it is built:
+    ``forward_<platform>`` if the subclass defines it, else ``forward_native``.
+    Subclasses pick their kernel from ``requested_implementation``."""
 
     op_name = "custom_op"
 
@@ -94,15 +98,3 @@ class CustomOp(nn.Module):
 
     def forward_xpu(self, *args: Any, **kwargs: Any) -> Any:
         return self.forward_native(*args, **kwargs)
-
-    def require_cuda_implementation(self, supported: set[str] | frozenset[str]) -> str:
-        """The requested provider name of this op, after the reference's two
-        checks: it must be one of ``supported`` (ValueError), and only "auto"
-        and the native names may be asked for off CUDA (RuntimeError)."""
-        choice = self.requested_implementation
-        if choice not in supported:
-            names = ", ".join(sorted(supported))
-            raise ValueError(f"unsupported {self.op_name!r} implementation {choice!r}; available: {names}")
-        if self.platform != "cuda" and choice != "auto" and choice not in NATIVE_IMPLEMENTATIONS:
-            raise RuntimeError(f"{choice!r} for {self.op_name!r} requires CUDA")
-        return choice

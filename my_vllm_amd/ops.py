@@ -348,10 +348,15 @@ def decode_workspace_bytes(num_part_slots: int, num_kv_heads: int, group: int) -
 DECODE_STORE_ERROR_OFFSET = 4224
 
 
+# (token, KV head) rows a fused store launch takes (its per-row flags).
+FUSED_STORE_MAX_ROWS = 65536
+
+
 def decode_store_error(workspace: torch.Tensor, clear: bool = True) -> bool:
     """Whether a :func:`paged_decode_store` launch on ``workspace`` met a row
-    whose slot is not in its sequence's last page (and skipped it).  Reads
-    the device, so it synchronizes with the stream; ``clear`` resets the word."""
+    whose slot is not its sequence's last position (the row was written after
+    the attention read the cache).  Reads the device, so it synchronizes with
+    the stream; ``clear`` resets the word."""
     word = workspace[DECODE_STORE_ERROR_OFFSET:DECODE_STORE_ERROR_OFFSET + 4].view(torch.int32)
     flagged = bool(word.item() != 0)
     if flagged and clear:
@@ -449,12 +454,16 @@ def paged_decode_store(
     """:func:`store_kvcache` of this step's ``key``/``value`` and :func:`paged_decode`
     in one launch (piece lists only).
 
-    Each new row lands in its sequence's last page, which only one piece per
-    KV head reads; that piece's wavefront writes the row before reading any
-    page.  A row whose slot is in another page is not written and sets the
-    workspace word at :data:`DECODE_STORE_ERROR_OFFSET` (see
-    :func:`decode_store_error`).  ``key``/``value`` are ``[T, Hkv, D]`` with
-    unit inner stride; ``slot_mapping`` int32/int64 ``[T]`` (``< 0`` = skip).
+    A new row whose slot is its sequence's last position lies in the last
+    page, which only one piece per KV head reads; that piece's wavefront
+    writes the row before reading any page.  Any other row with a slot >= 0
+    (a slot elsewhere, or a row no piece names) is written by the merge
+    kernel that always follows, after the attention has read the cache, and
+    sets the workspace word at :data:`DECODE_STORE_ERROR_OFFSET` (see
+    :func:`decode_store_error`).  So the caches always end as
+    :func:`store_kvcache` leaves them.  At most :data:`FUSED_STORE_MAX_ROWS`
+    (token, KV head) rows.  ``key``/``value`` are ``[T, Hkv, D]`` with unit
+    inner stride; ``slot_mapping`` int32/int64 ``[T]`` (``< 0`` = skip).
     """
     if validate:
         _check_paged(q, out, k_cache, v_cache,
@@ -625,6 +634,19 @@ def prefill_workspace_bytes(max_tiles: int) -> int:
     return nbytes
 
 
+# Byte offset of the prefill plan's dropped-tile count in a prefill workspace
+# (MVA_PREFILL_DROPPED_TILES_OFFSET in include/my_vllm_amd.h).
+PREFILL_DROPPED_TILES_OFFSET = 4
+
+
+def prefill_dropped_tiles(workspace: torch.Tensor) -> int:
+    """Tiles of the last :func:`paged_prefill` launch on ``workspace`` beyond
+    its ``max_tiles`` (not run; 0 when the bound held).  Reads the device, so
+    it synchronizes with the stream."""
+    off = PREFILL_DROPPED_TILES_OFFSET
+    return int(workspace[off:off + 4].view(torch.int32).item())
+
+
 def paged_prefill(
     q: torch.Tensor,
     k_cache: torch.Tensor,
@@ -645,7 +667,9 @@ def paged_prefill(
     The query tiles are planned on the device from ``query_start_loc`` and
     ``seq_lens`` into ``workspace`` (at least
     ``prefill_workspace_bytes(max_tiles)`` bytes); ``max_tiles`` must bound
-    the tile count (see :func:`prefill_max_tiles`).
+    the tile count (see :func:`prefill_max_tiles`): tiles beyond it are not
+    run and counted at :data:`PREFILL_DROPPED_TILES_OFFSET`
+    (:func:`prefill_dropped_tiles`).
     """
     if validate:
         _check_paged(q, out, k_cache, v_cache,

@@ -29,3 +29,13 @@ def assert_attention_close(actual: torch.Tensor, expected_fp32: torch.Tensor) ->
     assert actual.shape == expected.shape
     assert torch.isfinite(actual).all(), "non-finite attention output"
     torch.testing.assert_close(actual, expected, atol=ATTN_ATOL, rtol=ATTN_RTOL)
+
+
+def set_decode_planning(monkeypatch, waves=None, schedule=None) -> None:
+    """Override the decode wavefront count and schedule of every MI355X
+    backend for one test (the backends' planning-override attributes)."""
+    from my_vllm_amd.attention_backend import MI355XAttentionBackendMixin
+
+    monkeypatch.setattr(MI355XAttentionBackendMixin, "decode_waves_override",
+                        None if waves is None else int(waves))
+    monkeypatch.setattr(MI355XAttentionBackendMixin, "decode_schedule_override", schedule)

@@ -103,3 +103,32 @@ def test_planners_refuse_bad_input_like_the_statement():
     with pytest.raises(RuntimeError, match="capacity"):
         _native.call("mva_decode_plan_claims", counts.ctypes.data, 2, 0, 0, 8, 64, 1.5, 4, 128,
                      items.ctypes.data, 1, 0, 0, out.ctypes.data)
+
+
+def test_planners_refuse_indices_beyond_int32():
+    # Sequence and query-row indices are int32 in the pieces: the last
+    # sequence may sit at 2^31-1 but not past it.
+    top = 2**31 - 1
+    counts = np.array([3, 5], np.int64)
+    for first_seq, first_q_row in ((top, 0), (0, top), (top - 1, top + 5)):
+        with pytest.raises(RuntimeError, match="int32 range"):
+            plan_decode_claims(counts, first_seq, first_q_row, 8, 16)
+        with pytest.raises(RuntimeError, match="int32 range"):
+            plan_decode_listed(counts, first_seq, first_q_row, 8, 16)
+    items, _, _, _ = plan_decode_claims(counts, top - 1, top - 1, 8, 16)
+    assert items[:, 0].max() == top and items[:, 6].max() == top
+    items, _, _, _, _ = plan_decode_listed(counts, top - 1, top - 1, 8, 16)
+    assert items[:, 0].max() == top and items[:, 6].max() == top
+
+
+def test_claims_planner_refuses_more_than_int32_pieces():
+    # 3 segments of 2^31-1 pages at 64 KV heads and 128-page pieces: about
+    # 3.2e9 pieces.  Refused before anything is written (a 1-row buffer).
+    top = 2**31 - 1
+    counts = np.full(3, top, np.int64)
+    items = np.zeros((1, ops.DECODE_ITEM_INTS), np.int32)
+    out = np.zeros(4, np.int64)
+    with pytest.raises(RuntimeError, match="2\\^31-1 pieces"):
+        _native.call("mva_decode_plan_claims", counts.ctypes.data, 3, 0, 0, 64, 1, 1.0, 1, 128,
+                     items.ctypes.data, 1 << 40, 0, 0, out.ctypes.data)
+    assert not items.any() and not out.any()

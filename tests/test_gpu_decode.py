@@ -22,7 +22,7 @@ from my_vllm_amd.attention_backend import (
 from my_vllm_amd.contract import AttentionRoute, BatchType
 from workloads import config_decode_small, decode_lengths, make_paged_batch
 from oracle.reference import paged_attention
-from tests._util import assert_attention_close
+from tests._util import assert_attention_close, set_decode_planning
 
 pytestmark = pytest.mark.gpu
 
@@ -62,7 +62,7 @@ def test_reference_shapes(gpu):
 
 @pytest.mark.parametrize("schedule", ["listed", "claims"])
 def test_qwen3_0p6b_decode_configuration(gpu, monkeypatch, schedule):
-    monkeypatch.setenv("MVA_DECODE_SCHEDULE", schedule)
+    set_decode_planning(monkeypatch, schedule=schedule)
     batch = config_decode_small(seed=1)
     out, backend, plan, _ = _run(batch, gpu)
     assert (plan.metadata.decode_wave_extra is not None) == (schedule == "listed")
@@ -84,8 +84,7 @@ def test_split_k_merge(gpu, monkeypatch, waves, schedule):
     # piece (128-page pieces) itself; 100000 waves give 4-page pieces and one
     # wavefront per piece.  Piece lists: waves / 8 page ranges (at least
     # one), down to one page per range.
-    monkeypatch.setenv("MVA_DECODE_WAVES", str(waves))
-    monkeypatch.setenv("MVA_DECODE_SCHEDULE", schedule)
+    set_decode_planning(monkeypatch, waves=waves, schedule=schedule)
     ctx = [1, 16, 17, 255, 256, 257, 1000, 3001, 4096, 2049]
     batch = make_paged_batch(43, [1] * len(ctx), ctx, 0, 32, 8)
     out, backend, plan, args = _run(batch, gpu)
@@ -191,7 +190,7 @@ def test_merge_of_one_page_pieces_for_every_group_shape(gpu, hq, hkv):
 
 
 def test_stale_nan_rows_past_seq_len_do_not_leak(gpu, monkeypatch):
-    monkeypatch.setenv("MVA_DECODE_WAVES", "100000")
+    set_decode_planning(monkeypatch, waves=100000)
     ctx = [5, 16, 33, 300, 129]
     batch = make_paged_batch(47, [1] * len(ctx), ctx, 0, 16, 8, extra_pages=3)
     bt = batch.common.block_tables

@@ -17,7 +17,7 @@ from my_vllm_amd import ops
 from my_vllm_amd.attention_backend import MI355XAttentionBackend
 from my_vllm_amd.contract import AttentionRoute
 from workloads import config_decode_small, make_paged_batch
-from tests._util import assert_attention_close
+from tests._util import assert_attention_close, set_decode_planning
 from tests.test_gpu_prefill import expected, to_device
 
 pytestmark = pytest.mark.gpu
@@ -64,7 +64,7 @@ def test_page_boundaries_int64_slots_and_skips(gpu, hq, hkv):
 
 
 def test_claim_schedule_falls_back_to_the_separate_store(gpu, monkeypatch):
-    monkeypatch.setenv("MVA_DECODE_SCHEDULE", "claims")
+    set_decode_planning(monkeypatch, schedule="claims")
     batch = make_paged_batch(89, [1] * 5, [40, 7, 1000, 16, 129], 0, 32, 8)
     plan, sep, fused, (kc_a, vc_a), (kc_b, vc_b) = _both_ways(batch, gpu)
     assert plan.metadata.decode_wave_extra is None
@@ -74,33 +74,64 @@ def test_claim_schedule_falls_back_to_the_separate_store(gpu, monkeypatch):
     assert_attention_close(fused, expected(stored))
 
 
-def _moved_slot_batch():
-    # Sequence 2's new row is sent to a slot in its first page instead of
-    # its last one: a page the decode launch may be streaming elsewhere.
+def _moved_slot_batch(where="first_page"):
+    # Sequence 2's new row is sent to a slot in its first page (a page the
+    # decode launch may be streaming elsewhere), or to the wrong row of its
+    # last page, instead of its last position.
     batch = make_paged_batch(97, [1] * 5, [40, 7, 1000, 16, 129], 0, 16, 8)
     slots = batch.common.slot_mapping.clone()
-    first_page = int(batch.common.block_tables[2, 0])
-    slots[2] = first_page * 16 + 3
+    if where == "first_page":
+        slots[2] = int(batch.common.block_tables[2, 0]) * 16 + 3
+    else:
+        assert (1000 - 1) % 16 > 0
+        slots[2] = slots[2] - 1
     return batch, slots
 
 
-def test_slot_outside_the_last_page_is_skipped_and_flagged(gpu):
-    batch, slots = _moved_slot_batch()
+@pytest.mark.parametrize("where", ["first_page", "last_page_wrong_row"])
+def test_slot_outside_the_last_position_is_stored_late_and_flagged(gpu, where):
+    batch, slots = _moved_slot_batch(where)
     common, q, kc, vc = to_device(batch, gpu)
     k_new, v_new = batch.k_new.to(gpu), batch.v_new.to(gpu)
+    slots = slots.to(gpu)
     backend = MI355XAttentionBackend(16, 8, 128, 16, torch.bfloat16)
     plan = backend.build_plan(common)
     assert common.trusted and plan.metadata.decode_wave_extra is not None
-    fused = backend.forward_with_kv_store(q, k_new, v_new, kc, vc, slots.to(gpu), plan).clone()
+    fused = backend.forward_with_kv_store(q, k_new, v_new, kc, vc, slots, plan).clone()
     assert backend.fused_store_error() is True
     assert backend.fused_store_error() is False  # cleared by the first read
-    # Expected: every other row stored, the moved one not at all.
+    # The caches equal the reference's store of every row, the moved one included.
     kc_e, vc_e = batch.k_cache.to(gpu), batch.v_cache.to(gpu)
+    ops.store_kvcache(k_new, v_new, kc_e, vc_e, slots)
+    assert torch.equal(kc, kc_e) and torch.equal(vc, vc_e)
+    # The attention ran before the moved row was written.
+    kc_o, vc_o = batch.k_cache.to(gpu), batch.v_cache.to(gpu)
     keep = torch.ones(5, dtype=torch.bool, device=gpu)
     keep[2] = False
-    ops.store_kvcache(k_new[keep], v_new[keep], kc_e, vc_e, slots.to(gpu)[keep])
-    assert torch.equal(kc, kc_e) and torch.equal(vc, vc_e)
-    assert torch.equal(fused, backend.forward(q, k_new, v_new, kc_e, vc_e, plan))
+    ops.store_kvcache(k_new[keep], v_new[keep], kc_o, vc_o, slots[keep])
+    assert torch.equal(fused, backend.forward(q, k_new, v_new, kc_o, vc_o, plan))
+    # A second fused step on the same workspace: the late-row flags were
+    # cleared, so every in-place row is written by the decode again.
+    kc2, vc2 = batch.k_cache.to(gpu), batch.v_cache.to(gpu)
+    good = common.slot_mapping
+    again = backend.forward_with_kv_store(q, k_new, v_new, kc2, vc2, good, plan).clone()
+    assert backend.fused_store_error() is False
+    kc_g, vc_g = batch.k_cache.to(gpu), batch.v_cache.to(gpu)
+    ops.store_kvcache(k_new, v_new, kc_g, vc_g, good)
+    assert torch.equal(kc2, kc_g) and torch.equal(vc2, vc_g)
+    assert torch.equal(again, backend.forward(q, k_new, v_new, kc_g, vc_g, plan))
+
+
+def test_fused_store_debug_check_raises(gpu):
+    batch, slots = _moved_slot_batch()
+    common, q, kc, vc = to_device(batch, gpu)
+    backend = MI355XAttentionBackend(16, 8, 128, 16, torch.bfloat16)
+    backend.check_fused_store = True
+    plan = backend.build_plan(common)
+    k_new, v_new = batch.k_new.to(gpu), batch.v_new.to(gpu)
+    backend.forward_with_kv_store(q, k_new, v_new, kc, vc, common.slot_mapping, plan)  # in place: no error
+    with pytest.raises(RuntimeError, match="last position"):
+        backend.forward_with_kv_store(q, k_new, v_new, kc, vc, slots.to(gpu), plan)
 
 
 def test_untrusted_metadata_stores_first_like_the_reference(gpu):

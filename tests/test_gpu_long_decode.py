@@ -21,7 +21,7 @@ from my_vllm_amd import ops
 from my_vllm_amd.attention_backend import MI355XAttentionBackend
 from my_vllm_amd.contract import AttentionRoute
 from oracle.reference import paged_attention, silu_and_mul_fused
-from tests._util import assert_attention_close, max_ulp_diff
+from tests._util import assert_attention_close, max_ulp_diff, set_decode_planning
 from workloads import config_long_decode, silu_input
 
 pytestmark = pytest.mark.gpu
@@ -55,7 +55,7 @@ def _host_expected(batch, seqs):
 def test_qwen3_32b_long_decode_configuration(gpu, long_batch, monkeypatch, schedule):
     batch = long_batch
     if schedule == "listed":
-        monkeypatch.setenv("MVA_DECODE_SCHEDULE", "listed")
+        set_decode_planning(monkeypatch, schedule="listed")
     backend = MI355XAttentionBackend(64, 8, 128, 16, torch.bfloat16)
     plan = backend.build_plan(batch.common)
     assert plan.route is AttentionRoute.DECODE

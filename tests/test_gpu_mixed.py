@@ -15,7 +15,7 @@ import torch
 from my_vllm_amd.contract import AttentionRoute
 from my_vllm_amd.contract import BatchType
 from workloads import config_mixed, make_paged_batch
-from tests._util import assert_attention_close
+from tests._util import assert_attention_close, set_decode_planning
 from tests.test_gpu_prefill import expected, run_backend
 
 pytestmark = pytest.mark.gpu
@@ -23,7 +23,7 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("waves", ["3", "2048", "100000"])
 def test_mixed_unified_and_split_match(gpu, monkeypatch, waves):
-    monkeypatch.setenv("MVA_DECODE_WAVES", waves)
+    set_decode_planning(monkeypatch, waves=waves)
     q = [5, 130, 1, 1, 1, 1]
     kv = [21, 400, 13, 18, 1500, 3000]
     batch = make_paged_batch(83, q, kv, 2, 32, 8)
@@ -142,7 +142,7 @@ def test_mixed_in_launch_merges_flush_a_long_list(gpu, monkeypatch):
     # One decode wavefront runs 640 split pieces (40 sequences x 8 KV heads x
     # 2 chunks): its list of pieces awaiting arrival fills (64 entries) and
     # is flushed ten times; every segment is still merged exactly once.
-    monkeypatch.setenv("MVA_DECODE_WAVES", "1")
+    set_decode_planning(monkeypatch, waves=1)
     q = [40] + [1] * 40
     kv = [300] + [2080] * 40
     batch = make_paged_batch(103, q, kv, 1, 16, 8)
@@ -154,16 +154,33 @@ def test_mixed_in_launch_merges_flush_a_long_list(gpu, monkeypatch):
 
 def test_mixed_beyond_one_launch_runs_prefill_then_decode(gpu):
     # More prefill sequences than one MIXED launch orders (1024): the unified
-    # backend runs the batch as prefill + decode launches, with the same rows.
+    # backend plans MIXED_SPLIT, says why, and runs prefill + decode launches
+    # (reference attention_backend.py:626-663, 858-890).
     from my_vllm_amd import ops
+    from my_vllm_amd.attention_backend import MI355XAttentionBackend
+    from tests.test_gpu_prefill import to_device
 
     n = ops.MIXED_PREFILL_SEQS_MAX + 3
     q = [2] * n + [1, 1]
     kv = [9] * n + [300, 40]
     batch = make_paged_batch(107, q, kv, n, 16, 8)
-    out, plan = run_backend(batch, gpu)
-    assert plan.route is AttentionRoute.MIXED_UNIFIED and plan.metadata.mixed_prefill_max_tiles == 0
+    backend = MI355XAttentionBackend(16, 8, 128, 16, torch.bfloat16)
+    common, qd, kc, vc = to_device(batch, gpu)
+    plan = backend.build_plan(common)
+    assert plan.route is AttentionRoute.MIXED_SPLIT and plan.metadata.mixed_prefill_max_tiles == 0
+    assert backend.mixed_attention_available is False
+    assert f"at most {ops.MIXED_PREFILL_SEQS_MAX} prefill sequences" in backend.mixed_attention_unavailable_reason
+    assert dict(backend.route_counts)["mixed_split"] == 1 and dict(backend.route_counts)["mixed_unified"] == 0
+    empty = qd.new_empty((0, 8, 128))
+    out = backend.forward(qd, empty, empty, kc, vc, plan)
     assert_attention_close(out, expected(batch))
+    # A batch within the limits on the same backend runs as one launch again.
+    small = make_paged_batch(108, [5, 1], [21, 13], 1, 16, 8)
+    common, qd, kc, vc = to_device(small, gpu)
+    plan = backend.build_plan(common)
+    assert plan.route is AttentionRoute.MIXED_UNIFIED and backend.mixed_attention_available
+    assert backend.mixed_attention_unavailable_reason is None
+    assert_attention_close(backend.forward(qd, empty, empty, kc, vc, plan), expected(small))
 
 
 def test_mixed_after_decode_steps_on_one_workspace(gpu, monkeypatch):
@@ -185,9 +202,9 @@ def test_mixed_after_decode_steps_on_one_workspace(gpu, monkeypatch):
         # Default decode planning (many ranges, many partial slots); few
         # decode wavefronts in the MIXED launches (few partial slots).
         if b.common.num_prefill_seqs:
-            monkeypatch.setenv("MVA_DECODE_WAVES", "64")
+            set_decode_planning(monkeypatch, waves=64)
         else:
-            monkeypatch.delenv("MVA_DECODE_WAVES", raising=False)
+            set_decode_planning(monkeypatch)
         common, qd, kc, vc = to_device(b, gpu)
         plan = backend.build_plan(common)
         empty = qd.new_empty((0, 8, 128))

@@ -223,12 +223,36 @@ def test_device_tile_plan_is_exact(gpu, hq, hkv):
     tile = ops.PREFILL_STREAM_ROWS // (hq // hkv)
     want = _expected_tiles(q, kv, tile)
     assert int(backend_ws[0]) == len(want) <= p.metadata.prefill_max_tiles
+    assert ops.prefill_dropped_tiles(backend._prefill_workspace) == 0
     head, rec = ops.PREFILL_PLAN_HEADER_INTS, ops.PREFILL_PLAN_ITEM_INTS
     got = backend_ws[head:head + rec * len(want)].view(-1, rec).tolist()
     # Page slots -> the sequence's page ids.
     bt = batch.common.block_tables
     want = [r[:8] + [int(bt[r[0], i]) for i in r[8:]] for r in want]
     assert got == want
+
+
+def test_undersized_tile_bound_is_reported(gpu):
+    # A max_tiles below the batch's tile count (a host bound that disagrees
+    # with the device's query offsets): the tiles past it are not run, their
+    # rows keep the buffer's contents, and the plan reports how many.
+    q = [300, 37, 130, 64]
+    kv = [300 + 48, 37, 130, 64]
+    batch = make_paged_batch(139, q, kv, len(q), 32, 8)
+    common, qd, kc, vc = to_device(batch, gpu)
+    tile = ops.PREFILL_STREAM_ROWS // 4
+    n_tiles = len(_expected_tiles(q, kv, tile))
+    ws = torch.empty(ops.prefill_workspace_bytes(n_tiles), dtype=torch.uint8, device=gpu)
+    for cap, dropped in ((n_tiles, 0), (n_tiles - 3, 3), (1, n_tiles - 1)):
+        out = torch.full_like(qd, float("nan"))
+        ops.paged_prefill(qd, kc, vc, common.block_tables, common.seq_lens, common.query_start_loc, len(q), cap,
+                          ws, out, 128 ** -0.5)
+        assert ops.prefill_dropped_tiles(ws) == dropped
+        stale = torch.isnan(out.float()).all(dim=2)  # [tokens, heads]
+        assert bool(stale.any()) == (dropped > 0)
+        ref = expected(batch)
+        done = ~stale.cpu()
+        torch.testing.assert_close(out.float().cpu()[done], ref[done], atol=2e-2, rtol=1e-2)
 
 
 def test_more_sequences_than_the_planner_sorts(gpu):

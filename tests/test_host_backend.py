@@ -390,22 +390,86 @@ def test_prefill_tile_bounds_hold_for_any_split_of_the_tokens(seed):
         assert int(np.sum(-(-q // tile))) <= bound(int(q.sum()), n, hq, hkv)
 
 
-def test_mixed_beyond_one_launch_limits_runs_as_two_launches():
+def test_mixed_beyond_one_launch_limits_plans_mixed_split():
     # More prefill sequences than one MIXED launch takes: the unified
-    # backend plans the batch for prefill + decode launches.
+    # backend plans MIXED_SPLIT (prefill + decode launches) and names the
+    # limit, as the reference plans MIXED_SPLIT whenever it runs two
+    # launches (attention_backend.py:626-663, 858-890).
     backend = HostBackend(16, 4, 128, 16, torch.bfloat16)
+    assert backend.mixed_attention_available and backend.mixed_attention_unavailable_reason is None
     n = ops.MIXED_PREFILL_SEQS_MAX + 1
     common = _common((1,) * n + (1,), (5,) * n + (9,), n, trusted=True)
     plan = backend.build_plan(common)
-    assert plan.route is AttentionRoute.MIXED_UNIFIED
+    assert plan.route is AttentionRoute.MIXED_SPLIT
     assert plan.metadata.mixed_prefill_max_tiles == 0 and plan.metadata.prefill_max_tiles > 0
+    assert plan.metadata.num_decode_merges >= 0 and plan.metadata.decode_items is not None
+    assert backend.mixed_attention_available is False
+    assert f"{ops.MIXED_PREFILL_SEQS_MAX} prefill sequences" in backend.mixed_attention_unavailable_reason
     small = backend.build_plan(_common((5, 1), (21, 13), 1, trusted=True))
-    assert small.metadata.mixed_prefill_max_tiles > 0
-    # More KV heads than one MIXED launch's counters cover: two launches too.
+    assert small.route is AttentionRoute.MIXED_UNIFIED and small.metadata.mixed_prefill_max_tiles > 0
+    assert backend.mixed_attention_available and backend.mixed_attention_unavailable_reason is None
+    # More KV heads than one MIXED launch's counters cover: split from the start.
     wide = HostBackend(128, 128, 128, 16, torch.bfloat16)
     assert ops.MIXED_MAX_KV_HEADS < 128
+    assert not wide.mixed_attention_available and "KV heads" in wide.mixed_attention_unavailable_reason
     plan = wide.build_plan(_common((5, 1), (21, 13), 1, trusted=True))
-    assert plan.route is AttentionRoute.MIXED_UNIFIED and plan.metadata.mixed_prefill_max_tiles == 0
+    assert plan.route is AttentionRoute.MIXED_SPLIT and plan.metadata.mixed_prefill_max_tiles == 0
+    # Split mode: the reference's reason string.
+    split = HostSplitBackend(16, 4, 128, 16, torch.bfloat16)
+    assert split.mixed_attention_unavailable_reason == "unified mixed attention is disabled in split mode"
+
+
+def test_mixed_split_pair_limit_plans_mixed_split():
+    # A single MIXED launch merges at most MIXED_ARRIVAL_COUNTERS split-K
+    # (partial slot, KV head) pairs; a decode plan beyond that runs split.
+    backend = HostBackend(64, 64, 128, 16, torch.bfloat16)
+    backend.decode_waves_override = 100000  # 4-page pieces: many split segments
+    common = _common((5,) + (1,) * 300, (21,) + (2048,) * 300, 1, trusted=True)
+    plan = backend.build_plan(common)
+    assert plan.route is AttentionRoute.MIXED_SPLIT
+    assert "split-K" in backend.mixed_attention_unavailable_reason
+    assert plan.metadata.num_decode_merges > 0
+
+
+def _validate_dispatch_route(*, batch_type, planned_route, mixed_attention_available, expected_route="auto"):
+    """The reference's dispatch-benchmark rule (bench_attention_dispatch.py:208-230):
+    the planned route must equal the capability route."""
+    assert batch_type == "mixed"
+    capability = "mixed_unified" if mixed_attention_available else "mixed_split"
+    required = capability if expected_route == "auto" else expected_route
+    assert planned_route == required and planned_route == capability
+    return planned_route
+
+
+@pytest.mark.parametrize("case", ["within", "beyond_seqs", "split_mode", "wide"])
+def test_planned_route_equals_the_capability_route(case):
+    n = ops.MIXED_PREFILL_SEQS_MAX + 1
+    backend = {"within": HostBackend(16, 4, 128, 16, torch.bfloat16),
+               "beyond_seqs": HostBackend(16, 4, 128, 16, torch.bfloat16),
+               "split_mode": HostSplitBackend(16, 4, 128, 16, torch.bfloat16),
+               "wide": HostBackend(128, 128, 128, 16, torch.bfloat16)}[case]
+    common = (_common((1,) * n + (1,), (5,) * n + (9,), n, trusted=True) if case == "beyond_seqs"
+              else _common((5, 1), (21, 13), 1, trusted=True))
+    plan = backend.build_plan(common)
+    route = _validate_dispatch_route(batch_type=plan.batch_type.value, planned_route=plan.route.value,
+                                     mixed_attention_available=backend.mixed_attention_available)
+    assert route == ("mixed_unified" if case == "within" else "mixed_split")
+    assert (backend.mixed_attention_unavailable_reason is None) == (case == "within")
+    counts = dict(backend.route_counts)
+    assert counts[route] == 1 and sum(counts.values()) == 1
+
+
+def test_mixed_route_must_match_its_metadata():
+    # A MIXED_UNIFIED plan over metadata planned for two launches (or the
+    # reverse) is refused before any launch.
+    backend = HostBackend(16, 4, 128, 16, torch.bfloat16)
+    common = _common((5, 1), (21, 13), 1, trusted=True)
+    unified = backend.build_plan(common)
+    forced = AttentionPlan(unified.batch_type, AttentionRoute.MIXED_SPLIT, common, unified.metadata)
+    q = torch.zeros(6, 16, 128, dtype=torch.bfloat16)
+    cache = torch.zeros(3, 16, 4, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="does not match the planned metadata"):
+        backend.forward(q, None, None, cache, cache, forced)
 
 
 @pytest.mark.parametrize("seed", range(5))

@@ -86,6 +86,8 @@ def test_store_error_offset_matches_the_header_and_the_workspace_layout():
     assert f"#define MVA_DECODE_STORE_ERROR_OFFSET {ops.DECODE_STORE_ERROR_OFFSET}" in header
     # The word sits inside the scheduler area every decode workspace has.
     assert ops.DECODE_STORE_ERROR_OFFSET + 4 <= _native.query("mva_decode_workspace_bytes", 0, 8, 1)
+    assert f"#define MVA_PREFILL_DROPPED_TILES_OFFSET {ops.PREFILL_DROPPED_TILES_OFFSET}" in header
+    assert ops.PREFILL_DROPPED_TILES_OFFSET + 4 <= _native.query("mva_prefill_workspace_bytes", 0)
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

@@ -14,6 +14,7 @@ import torch
 
 from my_vllm_amd import _native, ops
 from my_vllm_amd.attention_backend import MI355XAttentionBackend
+from tests._util import set_decode_planning
 from tests.test_gpu_prefill import to_device
 from workloads import config_decode_small, decode_lengths, make_paged_batch
 
@@ -23,7 +24,7 @@ SCRATCH_BYTES = 64 << 20  # MVA_DECODE_STATIC_SCRATCH_BYTES
 
 
 def _decode_args(batch, device, monkeypatch, schedule):
-    monkeypatch.setenv("MVA_DECODE_SCHEDULE", schedule)
+    set_decode_planning(monkeypatch, schedule=schedule)
     hq, hkv = batch.q.shape[1], batch.k_cache.shape[2]
     common, q, kc, vc = to_device(batch, device)
     md = MI355XAttentionBackend(hq, hkv, 128, 16, torch.bfloat16).build_plan(common).metadata
