@@ -136,32 +136,18 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* __res
 // Persistent prefill: workgroup b serves KV head b % num_kv_heads (so head
 // h stays on XCD h when the head count divides 8).  The workgroups of a head
 // take tiles of the plan in order from that head's claim counter, one claim
-// ahead: the next tile is claimed when a tile starts and is known by the
-// time it ends, so the grid never waits on dispatch and faster CUs simply
-// run more tiles.
+// ahead (prefill_items_pingpong), so the grid never waits on dispatch and
+// faster CUs simply run more tiles.
 template <typename T>
 __global__ __launch_bounds__(kPrefillPPThreads) void paged_prefill_stream_kernel(PrefillParams p,
                                                                                  int32_t* __restrict__ plan) {
   __shared__ __attribute__((aligned(16))) uint8_t tiles[kPrefillPPLdsBytes];
-  __shared__ int claimed;
+  __shared__ int nextq[2];
   const int h = (int)(blockIdx.x % (uint32_t)p.num_kv_heads);
-  const int n = sload(plan, 0);
-  const int slot = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) & 3;
-  int* const ctr = plan + kPrefillPlanLineInts * (1 + h);
-  auto claim = [&]() { return __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
-  if (threadIdx.x == 0) claimed = claim();
-  __syncthreads();
-  int idx = claimed;
-  while (idx < n) {
-    const PrefillWork wk = plan_work_slot(plan, idx, slot);
-    int next = 0;
-    if (threadIdx.x == 0) next = claim();
-    prefill_core_pingpong<T>(p, wk, h, (lds_u8*)tiles);
-    __syncthreads();  // every wave is done with this tile's LDS before `claimed` changes
-    if (threadIdx.x == 0) claimed = next;
-    __syncthreads();
-    idx = claimed;
-  }
+  if (__builtin_amdgcn_readfirstlane((int)threadIdx.x >> 8) == 0)
+    prefill_items_pingpong<T, 0>(p, plan, h, (lds_u8*)tiles, (lds_i32*)nextq);
+  else
+    prefill_items_pingpong<T, 1>(p, plan, h, (lds_u8*)tiles, (lds_i32*)nextq);
 }
 
 int device_cu_count() {

@@ -52,67 +52,69 @@ __device__ inline PrefillWork plan_work_slot(const int32_t* plan, int idx, int s
   return wk;
 }
 
-// One work item.  `tiles` holds kPrefillPPBufs K tile buffers then as many
-// V tile buffers (kPrefillTileBytes each); tile x uses buffer x % kPrefillPPBufs.
-// pg0 / pg1 in wk are this wave's page slot (w % 4) of tiles 0 and 1.
-template <typename T>
-__device__ __attribute__((always_inline)) inline void prefill_core_pingpong(const PrefillParams& p,
-                                                                            const PrefillWork& wk, int h,
-                                                                            lds_u8* tiles) {
+typedef __attribute__((address_space(3))) int32_t lds_i32;
+
+// The items one workgroup claims, run back to back by one wave group (kGrp:
+// 0 = waves 0-3, 1 = waves 4-7; a compile-time constant, so that the K and
+// V cache pointers are not a run-time choice, which the compiler would serve
+// by copying the kernel argument block to scratch).  `tiles` holds
+// kPrefillPPBufs K tile buffers then as many V tile buffers
+// (kPrefillTileBytes each); `nextq` holds two LDS words through which
+// thread 0 publishes claimed plan indices: word 0 the first item, word 1
+// the successor of the item that starts next.
+//
+// Tiles are numbered across items: the tiles of an item that starts at
+// global tile G0 are G0 .. G0 + n - 1, and global tile x uses buffer
+// x % kPrefillPPBufs, so the copy stream runs on from one item into the
+// next.  While item A runs, its successor B is already claimed (its index
+// is read at A's start) and A's phases prepare B:
+//   * at A's first S phase each wave loads B's plan record (scalar loads,
+//     in an S phase so that no LDS wait waits behind them);
+//   * group 0 copies K(B, 0) at phase 2 max(n - 2, 1) and K(B, 1) at phase
+//     2 max(n - 1, 1), group 1 copies V(B, 0) at phase 2 max(n - 1, 2) when
+//     that phase exists (n >= 2); each is the earliest even phase at which
+//     the buffer's previous tile has been read for the last time and B's
+//     record is loaded;
+//   * every wave loads B's query fragments after its last QK of A (phase
+//     2n, or 3 for group 1 when n = 1), and thread 0 claims the item after B
+//     at phase 2n;
+//   * at the end of A's last phase every wave waits for all of these, thread
+//     0 publishes the new claim, and one barrier separates A from B.
+// So B starts with its queries and first tiles resident and its successor
+// known: no plan read, query load, copy wait or claim sits between items.
+// Only when A has a single tile does group 1 copy V(B, 0) at B's start
+// (it is first read at B's phase 2, after the wait that ends phase 1).
+template <typename T, int kGrp>
+__device__ __attribute__((always_inline)) inline void prefill_items_pingpong(const PrefillParams& p, int32_t* plan,
+                                                                             int h, lds_u8* tiles, lds_i32* nextq) {
   typedef typename Elem<T>::v8 V8;
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // 0..7
-  const int grp = w >> 2;
   const int slot = w & 3;  // page slot this wave copies
   const int lane = tid & 63;
   const int ln = lane & 31;
   const int hi = lane >> 5;
-
-  const int s = wk.s;
-  const int t0 = wk.t0;
-  const int q0 = wk.q0;
-  const int q_len = wk.q_len;
-  const int kv = wk.kv;
   const int G = p.group;
   const int BMT = p.tile_tokens;  // 256 / G
-  const int base_pos = kv - q_len;
-  const int n = wk.ntiles;
-  const int full_tiles = wk.full_tiles;
+  const int n_items = sload(plan, 0);
+  int* const ctr = plan + kPrefillPlanLineInts * (1 + h);
+  auto claim = [&]() { return __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
 
-  // This lane's query row.
+  // This lane's query row of every item: head g of the KV head, token rr of
+  // the item's 256 / G tokens.
   const int R = 32 * w + ln;
   const int g = R / BMT;
-  const int tq = t0 + R % BMT;
-  const bool row_ok = g < G && tq < q_len;
-  const int pos = row_ok ? base_pos + tq : -1;  // keys j <= pos are visible
-
-  V8 qf[8];
-  {
-    const int row_tok = q0 + (row_ok ? tq : 0);
-    const int head = h * G + (g < G ? g : 0);
-    const T* qp = (const T*)p.q + (int64_t)row_tok * p.q_tok_stride + (int64_t)head * p.q_head_stride;
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) qf[kk] = row_ok ? ld16<V8>(qp + 8 * (2 * kk + hi)) : V8{};
-  }
+  const int rr = R % BMT;
 
   // Copies: group 0 fills K tiles, group 1 V tiles, wave w page slot w % 4.
-  const int32_t* bt = p.block_tables + (int64_t)s * p.bt_stride;
-  const int npages = wk.npages;
-  auto page_of = [&](int tile) {
-    const int pg = sload(bt, min(tile * (kPrefillKeys / kPageSize) + slot, npages - 1));
-    return (pg >= 0 && pg < p.num_pages) ? pg : 0;
-  };
   const uint32_t koff = (uint32_t)(((lane & 15) * p.tok_stride + 8 * (lane >> 4)) * (int64_t)sizeof(T));
   const uint32_t voff = (uint32_t)(((lane >> 2) * p.tok_stride + 8 * (lane & 3)) * (int64_t)sizeof(T));
-  auto kbuf = [&](int tile) { return tiles + (tile % kPrefillPPBufs) * kPrefillTileBytes; };
-  auto vbuf = [&](int tile) { return tiles + (kPrefillPPBufs + tile % kPrefillPPBufs) * kPrefillTileBytes; };
-  // The group is a compile-time constant here: a run-time choice between the
-  // K and V cache pointers would make the compiler index the kernel argument
-  // block and copy it to scratch.
-  auto copy_page = [&](int tile, int page, auto grp_tag) __attribute__((always_inline)) {
-    constexpr int kGrp = decltype(grp_tag)::value;
+  auto kbuf = [&](int x) { return tiles + (x % kPrefillPPBufs) * kPrefillTileBytes; };
+  auto vbuf = [&](int x) { return tiles + (kPrefillPPBufs + x % kPrefillPPBufs) * kPrefillTileBytes; };
+  // This wave's page of K (group 0) or V (group 1) of global tile x.
+  auto copy_page = [&](int x, int page) __attribute__((always_inline)) {
     const T* src = (const T*)(kGrp == 0 ? p.k_cache : p.v_cache) + h * kHeadDim;
-    lds_u8* buf = kGrp == 0 ? kbuf(tile) : vbuf(tile);
+    lds_u8* buf = kGrp == 0 ? kbuf(x) : vbuf(x);
     dma16_x4_saddr(src + (int64_t)__builtin_amdgcn_readfirstlane(page) * p.page_stride, kGrp == 0 ? koff : voff,
                    (uint32_t)(uintptr_t)(buf + 4096 * slot));
   };
@@ -130,12 +132,25 @@ __device__ __attribute__((always_inline)) inline void prefill_core_pingpong(cons
                                                           7));
   };
 
+  V8 qf[8];
+  // Query fragments of item `it` (rows past the sequence or the heads read
+  // zeros).
+  auto load_q = [&](const PrefillWork& it) __attribute__((always_inline)) {
+    const int tq = it.t0 + rr;
+    const bool ok = g < G && tq < it.q_len;
+    const int row_tok = it.q0 + (ok ? tq : 0);
+    const int head = h * G + (g < G ? g : 0);
+    const T* qp = (const T*)p.q + (int64_t)row_tok * p.q_tok_stride + (int64_t)head * p.q_head_stride;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) qf[kk] = ok ? ld16<V8>(qp + 8 * (2 * kk + hi)) : V8{};
+  };
+
   f32x16 o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{};
   f32x16 st[2];  // S(t): st[mt][i] = S[query ln][key 32*mt + 8*(i/4) + 4*hi + i%4]
   u32x4 pw[4];   // P(t) for PV k-step kk: four packed pairs
-  float m = -INFINITY;  // reference max (log2 units) of the tiles so far
+  float m = -INFINITY;  // reference max (log2 units) of the item's tiles so far
   float l = 0.f;        // row sum of P relative to m
 
   // Phase fences for the compiler.  A barrier orders memory only: without
@@ -150,104 +165,6 @@ __device__ __attribute__((always_inline)) inline void prefill_core_pingpong(cons
   auto pin_o = [&]() __attribute__((always_inline)) {
     asm volatile("" : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]));
   };
-
-  // M phase t: PV(t-1) and QK(t), alternating, fragment reads one step ahead.
-  auto phase_m = [&](int t, auto with_qk_tag, auto with_pv_tag) __attribute__((always_inline)) {
-    constexpr bool with_qk = decltype(with_qk_tag)::value;
-    constexpr bool with_pv = decltype(with_pv_tag)::value;
-    if constexpr (with_pv) pin_p();
-    const lds_u8* kb = kbuf(t);
-    const lds_u8* vb = vbuf(t + kPrefillPPBufs - 1);  // V(t-1)
-    V8 kf[2], vf[2];
-    if constexpr (with_qk) {
-      kf[0] = kread(kb, 0);
-      st[0] = f32x16{};
-      st[1] = f32x16{};
-    }
-    if constexpr (with_pv) vf[0] = vread(vb, 0);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      if constexpr (with_qk) {
-        if (j + 1 < 16) kf[(j + 1) & 1] = kread(kb, j + 1);
-        st[j & 1] = Elem<T>::mfma32(kf[j & 1], qf[j >> 1], st[j & 1]);
-      }
-      if constexpr (with_pv) {
-        if (j + 1 < 16) vf[(j + 1) & 1] = vread(vb, j + 1);
-        o[j & 3] = Elem<T>::mfma32(vf[j & 1], __builtin_bit_cast(V8, pw[j >> 2]), o[j & 3]);
-      }
-      // Keeps the fragment reads one step ahead instead of all at the top,
-      // which would hold 48 fragments in registers at once.
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if constexpr (with_qk) pin_s();
-    if constexpr (with_pv) pin_o();
-  };
-
-  // S phase t: softmax of S(t) into P(t).
-  auto phase_s = [&](int t) __attribute__((always_inline)) {
-    pin_s();
-    if (t >= full_tiles) {
-      // Key t*64 + 32*mt + 8*(i/4) + 4*hi + i%4 is visible when
-      // 32*mt + 8*(i/4) + i%4 <= lim.  lim and S pass through an empty asm
-      // statement so that the compares and selects stay inside this branch:
-      // hoisted, they would run on every tile and hold 32 compare masks in
-      // scalar registers.
-      int lim = pos - t * kPrefillKeys - 4 * hi;
-      asm volatile("" : "+v"(lim), "+v"(st[0]), "+v"(st[1]));
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (32 * mt + 8 * (i >> 2) + (i & 3) > lim) st[mt][i] = -INFINITY;
-    }
-    // Row max with the IEEE maximum (v_maximum3_f32), which needs no quieting
-    // of MFMA-produced inputs, unlike fmaxf.
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; i += 2)
-        tmax = __builtin_elementwise_maximum(__builtin_elementwise_maximum(tmax, st[mt][i]), st[mt][i + 1]);
-    // The reference max moves only when it grows by more than 8 (log2
-    // units): P stays <= 2^8 and most tiles skip the O rescale.
-    const float tmax_s = pair_max(tmax) * p.scale_log2;  // scale > 0 commutes with max
-    const bool grow = tmax_s > m + 8.0f;
-    const float m_new = grow ? tmax_s : m;
-    const float alpha = grow ? fast_exp2(m - m_new) : 1.0f;  // m = -inf -> 0
-    m = m_new;
-    const float m_use = (m == -INFINITY) ? 0.f : m;
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
-      l *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
-    }
-    float la = 0.f, lb = 0.f;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {  // element pair q: elements 2q, 2q + 1
-      const int mt = q >> 3, i = 2 * (q & 7);
-      const float e0 = fast_exp2(st[mt][i] * p.scale_log2 - m_use);
-      const float e1 = fast_exp2(st[mt][i + 1] * p.scale_log2 - m_use);
-      pw[2 * mt + (q & 7) / 4][((i >> 2) & 1) * 2 + ((i & 3) >> 1)] = PackedPair<T>::pack(e0, e1);
-      la += e0;
-      lb += e1;
-    }
-    l += la + lb;
-    pin_p();
-  };
-
-  // Zero V rows of keys >= kv in the last tile (stale rows may hold NaN and
-  // 0 * NaN would leak through P = 0).
-  auto zero_tail = [&](int tile) __attribute__((always_inline)) {
-    lds_u8* vb = vbuf(tile);
-    const int first_bad = kv - tile * kPrefillKeys;  // rows >= first_bad are past the sequence
-    for (int i = tid; i < (kPrefillKeys - first_bad) * 16; i += kPrefillPPThreads) {
-      const int key = first_bad + (i >> 4);
-      lds_st16<u32x4>(vb + vlds_blk_off(key, i & 15), u32x4{0, 0, 0, 0});
-    }
-  };
-
-  const std::true_type yes;
-  const std::false_type no;
   // A workgroup barrier that also closes the phase for the instruction
   // scheduler (s_barrier alone lets register-only work move across it).
   auto phase_barrier = [&]() __attribute__((always_inline)) {
@@ -255,55 +172,247 @@ __device__ __attribute__((always_inline)) inline void prefill_core_pingpong(cons
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
   };
+  // Waits until at most the last c page copies (4 loads each) are in flight.
+  auto wait_copies = [&](int c) __attribute__((always_inline)) {
+    if (c >= 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(8));
+    else if (c == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm(4));
+    else __builtin_amdgcn_s_waitcnt(kVmcnt0);
+  };
 
-  // Prologue: K(0), K(1) (group 0) and V(0) (group 1) resident before
-  // phase 0.
-  if (grp == 0) {
-    copy_page(0, wk.pg0, std::integral_constant<int, 0>{});
-    if (1 < n) copy_page(1, wk.pg1, std::integral_constant<int, 0>{});
+  // ---- the first item ---------------------------------------------------------
+  if (tid == 0) nextq[0] = claim();
+  __syncthreads();
+  int idx = __builtin_amdgcn_readfirstlane(nextq[0]);
+  if (idx >= n_items) return;  // uniform: nothing for this workgroup
+  PrefillWork cur = plan_work_slot(plan, idx, slot);
+  int claim_ret = 0;  // thread 0: the latest claim
+  if (tid == 0) claim_ret = claim();
+  load_q(cur);
+  if constexpr (kGrp == 0) {
+    copy_page(0, cur.pg0);
+    if (1 < cur.ntiles) copy_page(1, cur.pg1);
   } else {
-    copy_page(0, wk.pg0, std::integral_constant<int, 1>{});
+    copy_page(0, cur.pg0);
   }
   __builtin_amdgcn_s_waitcnt(kVmcnt0);
+  if (tid == 0) nextq[1] = claim_ret;
   phase_barrier();
+  int G0 = 0;            // global index of the item's tile 0
+  bool v0_done = true;   // V of the item's tile 0 is copied (group 1)
 
-  // Phases 0 .. 2n+1.  At phase 2t group 0 copies K(t+2) and group 1 V(t+1)
-  // (three buffers each: the buffer written was last read in phase 2t-1),
-  // and every wave waits for its copies of phase 2t-2 at the end of phase
-  // 2t+1, before the barrier that opens their first reader's phase 2t+2; so
-  // a copy has two phase pairs to land.  pg_next is the page id of this
-  // wave's next copy; it is loaded at the start of an S phase (no LDS reads
-  // there to wait behind the scalar load) and used at the next even phase.
-  // V(n-1) lands by the end of phase 2n-1 and is first read in phase 2n
-  // (group 0's M(n)): its stale tail rows are cleared between them.  Both
-  // groups pass the same barriers.  Each group runs its own copy of the
-  // schedule (the group is a compile-time constant inside), so no value has
-  // to meet in the same registers on both groups' paths, and M(0) (no PV)
-  // and M(n) (no QK) are peeled off the loop so the loop body holds one copy
-  // of each phase.
-  const bool tail = n * kPrefillKeys > kv;
-  // End of phase 2t+1; `issued` says whether this wave copied at phase 2t
-  // (those 4 copies may stay in flight; vmcnt counts in issue order).
-  auto end_odd_phase = [&](int t, bool issued) __attribute__((always_inline)) {
-    if (issued) __builtin_amdgcn_s_waitcnt(waitcnt_vm(4));
-    else __builtin_amdgcn_s_waitcnt(kVmcnt0);
-    phase_barrier();
-    if (t == n - 1 && tail) {
-      zero_tail(n - 1);
-      phase_barrier();
+  const std::true_type yes;
+  const std::false_type no;
+  while (true) {
+    const int nidx = __builtin_amdgcn_readfirstlane(nextq[1]);
+    const bool has_next = nidx < n_items;
+    const int n = cur.ntiles;
+    const int full_tiles = cur.full_tiles;
+    const int kv = cur.kv;
+    const int tq = cur.t0 + rr;
+    const bool row_ok = g < G && tq < cur.q_len;
+    const int pos = row_ok ? kv - cur.q_len + tq : -1;  // keys j <= pos are visible
+    const int32_t* bt = p.block_tables + (int64_t)cur.s * p.bt_stride;
+    const int npages = cur.npages;
+    auto page_of = [&](int tile) {
+      const int pg = sload(bt, min(tile * (kPrefillKeys / kPageSize) + slot, npages - 1));
+      return (pg >= 0 && pg < p.num_pages) ? pg : 0;
+    };
+    PrefillWork nx;  // B's record, loaded at this item's first S phase
+    nx.ntiles = 0;
+    auto load_next = [&]() __attribute__((always_inline)) {
+      if (has_next) nx = plan_work_slot(plan, nidx, slot);
+    };
+    if constexpr (kGrp == 1) {
+      if (!v0_done) copy_page(G0, cur.pg0);
     }
-  };
-  auto run = [&](auto grp_tag) __attribute__((always_inline)) {
-    constexpr int kGrp = decltype(grp_tag)::value;
-    // Tile copied at phase 2t: c(t) = t + 2 (K) or t + 1 (V).
-    constexpr int kAhead = kGrp == 0 ? 2 : 1;
-    int pg_next = kGrp == 0 ? page_of(2) : __builtin_amdgcn_readfirstlane(wk.pg1);
+    m = -INFINITY;
+    l = 0.f;
+
+    // M phase t: PV(t-1) and QK(t), alternating, fragment reads one step ahead.
+    auto phase_m = [&](int t, auto with_qk_tag, auto with_pv_tag) __attribute__((always_inline)) {
+      constexpr bool with_qk = decltype(with_qk_tag)::value;
+      constexpr bool with_pv = decltype(with_pv_tag)::value;
+      if constexpr (with_pv) pin_p();
+      const lds_u8* kb = kbuf(G0 + t);
+      const lds_u8* vb = vbuf(G0 + t + kPrefillPPBufs - 1);  // V(t-1)
+      V8 kf[2], vf[2];
+      if constexpr (with_qk) {
+        kf[0] = kread(kb, 0);
+        st[0] = f32x16{};
+        st[1] = f32x16{};
+      }
+      if constexpr (with_pv) vf[0] = vread(vb, 0);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        if constexpr (with_qk) {
+          if (j + 1 < 16) kf[(j + 1) & 1] = kread(kb, j + 1);
+          st[j & 1] = Elem<T>::mfma32(kf[j & 1], qf[j >> 1], st[j & 1]);
+        }
+        if constexpr (with_pv) {
+          if (j + 1 < 16) vf[(j + 1) & 1] = vread(vb, j + 1);
+          o[j & 3] = Elem<T>::mfma32(vf[j & 1], __builtin_bit_cast(V8, pw[j >> 2]), o[j & 3]);
+        }
+        // Keeps the fragment reads one step ahead instead of all at the top,
+        // which would hold 48 fragments in registers at once.
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if constexpr (with_qk) pin_s();
+      if constexpr (with_pv) pin_o();
+    };
+
+    // S phase t: softmax of S(t) into P(t).
+    //
+    // Fast path (tiles after the first): P = exp2(S * scale - m) with the
+    // reference max as it stands, no row max.  It stands for this tile exactly
+    // when no element exceeds it by more than 8, and a row sum below 128 shows
+    // that for every element of the lane (each P is >= 0, and P < 128 means
+    // S * scale - m < 7.01, short of m + 8 by more than the rounding of
+    // S * scale and m + 8 while |m| < 2^20).  A row whose max is still -inf
+    // qualifies only when the tile masks all its keys (pos < 64 t): then P is
+    // 0 either way.  When every lane of the wave qualifies, P, l and m are
+    // bit for bit those of the full path below; otherwise the full path runs
+    // (row max, reference-max update, O rescale) and overwrites P.
+    auto phase_s = [&](int t) __attribute__((always_inline)) {
+      pin_s();
+      bool fast = false;
+      if (t >= full_tiles) {
+        // Key t*64 + 32*mt + 8*(i/4) + 4*hi + i%4 is visible when
+        // 32*mt + 8*(i/4) + i%4 <= lim.  lim and S pass through an empty asm
+        // statement so that the compares and selects stay inside this branch:
+        // hoisted, they would run on every tile and hold 32 compare masks in
+        // scalar registers.
+        int lim = pos - t * kPrefillKeys - 4 * hi;
+        asm volatile("" : "+v"(lim), "+v"(st[0]), "+v"(st[1]));
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            if (32 * mt + 8 * (i >> 2) + (i & 3) > lim) st[mt][i] = -INFINITY;
+      }
+      if (t > 0) {
+        const float m_fast = (m == -INFINITY) ? 0.f : m;
+        float la = 0.f, lb = 0.f;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int mt = q >> 3, i = 2 * (q & 7);
+          const float e0 = fast_exp2(st[mt][i] * p.scale_log2 - m_fast);
+          const float e1 = fast_exp2(st[mt][i + 1] * p.scale_log2 - m_fast);
+          pw[2 * mt + (q & 7) / 4][((i >> 2) & 1) * 2 + ((i & 3) >> 1)] = PackedPair<T>::pack(e0, e1);
+          la += e0;
+          lb += e1;
+        }
+        const float lt = la + lb;
+        const bool ok = __builtin_fabsf(m) < 0x1p20f ? lt < 128.f : (m == -INFINITY && pos < t * kPrefillKeys);
+        fast = !__builtin_amdgcn_ballot_w64(!ok);
+        if (fast) l += lt;
+      }
+      if (!fast) {
+        // Row max with the IEEE maximum (v_maximum3_f32), which needs no
+        // quieting of MFMA-produced inputs, unlike fmaxf.
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int i = 0; i < 16; i += 2)
+            tmax = __builtin_elementwise_maximum(__builtin_elementwise_maximum(tmax, st[mt][i]), st[mt][i + 1]);
+        // The reference max moves only when it grows by more than 8 (log2
+        // units): P stays <= 2^8 and most tiles skip the O rescale.
+        const float tmax_s = pair_max(tmax) * p.scale_log2;  // scale > 0 commutes with max
+        const bool grow = tmax_s > m + 8.0f;
+        const float m_new = grow ? tmax_s : m;
+        const float alpha = grow ? fast_exp2(m - m_new) : 1.0f;  // m = -inf -> 0
+        m = m_new;
+        const float m_use = (m == -INFINITY) ? 0.f : m;
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+          l *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+        }
+        float la = 0.f, lb = 0.f;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {  // element pair q: elements 2q, 2q + 1
+          const int mt = q >> 3, i = 2 * (q & 7);
+          const float e0 = fast_exp2(st[mt][i] * p.scale_log2 - m_use);
+          const float e1 = fast_exp2(st[mt][i + 1] * p.scale_log2 - m_use);
+          pw[2 * mt + (q & 7) / 4][((i >> 2) & 1) * 2 + ((i & 3) >> 1)] = PackedPair<T>::pack(e0, e1);
+          la += e0;
+          lb += e1;
+        }
+        l += la + lb;
+      }
+      pin_p();
+    };
+
+    // Zero V rows of keys >= kv in the item's last tile (stale rows may hold
+    // NaN and 0 * NaN would leak through P = 0).
+    auto zero_tail = [&]() __attribute__((always_inline)) {
+      lds_u8* vb = vbuf(G0 + n - 1);
+      const int first_bad = kv - (n - 1) * kPrefillKeys;  // rows >= first_bad are past the sequence
+      for (int i = tid; i < (kPrefillKeys - first_bad) * 16; i += kPrefillPPThreads) {
+        const int key = first_bad + (i >> 4);
+        lds_st16<u32x4>(vb + vlds_blk_off(key, i & 15), u32x4{0, 0, 0, 0});
+      }
+    };
+
+    // Copies this wave issues at phase 2t, and their number: this item's
+    // K(t+2) (group 0) or V(t+1) (group 1), and B's first tiles at the
+    // phases given above.
+    int pg_next = 0;  // page id of this wave's next copy of this item
+    auto issue = [&](int t) __attribute__((always_inline)) {
+      int c = 0;
+      if constexpr (kGrp == 0) {
+        if (t + 2 < n) {
+          copy_page(G0 + t + 2, pg_next);
+          ++c;
+        }
+        if (has_next && t == max(n - 2, 1)) {
+          copy_page(G0 + n, nx.pg0);
+          ++c;
+        }
+        if (has_next && t == max(n - 1, 1) && 1 < nx.ntiles) {
+          copy_page(G0 + n + 1, nx.pg1);
+          ++c;
+        }
+      } else {
+        if (t + 1 < n) {
+          copy_page(G0 + t + 1, pg_next);
+          ++c;
+        }
+        if (has_next && n >= 2 && t == max(n - 1, 2)) {
+          copy_page(G0 + n, nx.pg0);
+          ++c;
+        }
+      }
+      return c;
+    };
+
+    // Phases 0 .. 2n+1.  At phase 2t group 0 copies K(t+2) and group 1 V(t+1)
+    // (three buffers each: the buffer written was last read in phase 2t-1),
+    // and every wave waits for its copies of phase 2t-2 at the end of phase
+    // 2t+1, before the barrier that opens their first reader's phase 2t+2; so
+    // a copy has two phase pairs to land.  pg_next is loaded at the start of
+    // an S phase (no LDS reads there to wait behind the scalar load) and used
+    // at the next even phase.  V(n-1) lands by the end of phase 2n-1 and is
+    // first read in phase 2n (group 0's M(n)): its stale tail rows are
+    // cleared between them.  Both groups pass the same barriers.  M(0) (no
+    // PV) and M(n) (no QK) are peeled off the loop so the loop body holds one
+    // copy of each phase.
+    const bool tail = n * kPrefillKeys > kv;
+    auto end_odd_phase = [&](int t, int c) __attribute__((always_inline)) {
+      wait_copies(c);
+      phase_barrier();
+      if (t == n - 1 && tail) {
+        zero_tail();
+        phase_barrier();
+      }
+    };
     // Phases 0 and 1.
-    const bool issued0 = kAhead < n;
-    if (issued0) copy_page(kAhead, pg_next, grp_tag);
+    pg_next = kGrp == 0 ? page_of(2) : __builtin_amdgcn_readfirstlane(cur.pg1);
+    int c = issue(0);
     if constexpr (kGrp == 0) {
       phase_m(0, yes, no);
       phase_barrier();
+      load_next();
       pg_next = page_of(3);
       phase_s(0);
     } else {
@@ -311,52 +420,70 @@ __device__ __attribute__((always_inline)) inline void prefill_core_pingpong(cons
       phase_barrier();
       phase_m(0, yes, no);
     }
-    end_odd_phase(0, issued0);
+    end_odd_phase(0, c);
     // Phases 2t and 2t+1, t = 1 .. n-1.
     for (int t = 1; t < n; ++t) {
-      const bool issued = t + kAhead < n;
-      if (issued) copy_page(t + kAhead, pg_next, grp_tag);
+      c = issue(t);
       if constexpr (kGrp == 0) {
         phase_m(t, yes, yes);
         phase_barrier();
         pg_next = page_of(t + 3);
         phase_s(t);
       } else {
+        if (t == 1) load_next();
         pg_next = page_of(t + 2);
         phase_s(t - 1);
         phase_barrier();
         phase_m(t, yes, yes);
       }
-      end_odd_phase(t, issued);
+      end_odd_phase(t, c);
     }
-    // Phases 2n and 2n+1.
+    // Phases 2n and 2n+1; then every copy, query load and claim of this item
+    // has landed, and thread 0 publishes the claim.
     if constexpr (kGrp == 0) {
+      if (has_next) {
+        load_q(nx);
+        if (tid == 0) claim_ret = claim();
+      }
+      issue(n);
       phase_m(n, no, yes);
       phase_barrier();
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);
+      if (tid == 0 && has_next) nextq[1] = claim_ret;
     } else {
+      if (n == 1) load_next();
+      issue(n);
+      if (has_next && n >= 2) load_q(nx);
       phase_s(n - 1);
       phase_barrier();
+      if (has_next && n == 1) load_q(nx);
       phase_m(n, no, yes);
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);
     }
     phase_barrier();
-  };
-  if (grp == 0) run(std::integral_constant<int, 0>{});
-  else run(std::integral_constant<int, 1>{});
 
-  // Epilogue: O^T / l -> out[token][head][d].
-  const float l_tot = pair_sum(l);
-  if (!row_ok) return;
-  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-  T* op = (T*)p.out + (int64_t)(q0 + tq) * p.out_tok_stride + (int64_t)(h * G + g) * p.out_head_stride;
+    // Epilogue: O^T / l -> out[token][head][d].
+    const float l_tot = pair_sum(l);
+    if (row_ok) {
+      const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+      T* op = (T*)p.out + (int64_t)(cur.q0 + tq) * p.out_tok_stride + (int64_t)(h * G + g) * p.out_head_stride;
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+      for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-    for (int bk = 0; bk < 4; ++bk) {
-      typename Elem<T>::v4 wv;
+        for (int bk = 0; bk < 4; ++bk) {
+          typename Elem<T>::v4 wv;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) wv[e] = (T)(o[dt][4 * bk + e] * inv);
-      *reinterpret_cast<typename Elem<T>::v4*>(op + 32 * dt + 8 * bk + 4 * hi) = wv;
+          for (int e = 0; e < 4; ++e) wv[e] = (T)(o[dt][4 * bk + e] * inv);
+          *reinterpret_cast<typename Elem<T>::v4*>(op + 32 * dt + 8 * bk + 4 * hi) = wv;
+        }
     }
+    if (!has_next) return;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{};
+    G0 += n;
+    v0_done = n >= 2;
+    cur = nx;
+  }
 }
 
 }  // namespace mva
