@@ -137,12 +137,13 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* __res
 // h stays on XCD h when the head count divides 8).  The workgroups of a head
 // take tiles of the plan in order from that head's claim counter, one claim
 // ahead (prefill_items_pingpong), so the grid never waits on dispatch and
-// faster CUs simply run more tiles.
+// faster CUs simply run more tiles; once their head's queue is exhausted
+// they take the remaining tiles of the other heads.
 template <typename T>
 __global__ __launch_bounds__(kPrefillPPThreads) void paged_prefill_stream_kernel(PrefillParams p,
                                                                                  int32_t* __restrict__ plan) {
   __shared__ __attribute__((aligned(16))) uint8_t tiles[kPrefillPPLdsBytes];
-  __shared__ int nextq[2];
+  __shared__ int nextq[4];
   const int h = (int)(blockIdx.x % (uint32_t)p.num_kv_heads);
   if (__builtin_amdgcn_readfirstlane((int)threadIdx.x >> 8) == 0)
     prefill_items_pingpong<T, 0>(p, plan, h, (lds_u8*)tiles, (lds_i32*)nextq);

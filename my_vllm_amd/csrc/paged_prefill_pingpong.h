@@ -59,9 +59,16 @@ typedef __attribute__((address_space(3))) int32_t lds_i32;
 // V cache pointers are not a run-time choice, which the compiler would serve
 // by copying the kernel argument block to scratch).  `tiles` holds
 // kPrefillPPBufs K tile buffers then as many V tile buffers
-// (kPrefillTileBytes each); `nextq` holds two LDS words through which
-// thread 0 publishes claimed plan indices: word 0 the first item, word 1
-// the successor of the item that starts next.
+// (kPrefillTileBytes each); `nextq` holds four LDS words through which
+// thread 0 publishes claimed items: words 0 / 3 the first item's plan
+// index and KV head, words 1 / 2 those of the successor of the item that
+// starts next.
+//
+// Claims: a workgroup of KV head h0 claims from h0's counter.  Once that
+// queue is exhausted it claims from the following heads' counters in turn
+// (their items then run here, with their own K/V and output columns), so
+// that the workgroups of a head served by a faster XCD take over the last
+// items of slower heads instead of idling.
 //
 // Tiles are numbered across items: the tiles of an item that starts at
 // global tile G0 are G0 .. G0 + n - 1, and global tile x uses buffer
@@ -86,7 +93,7 @@ typedef __attribute__((address_space(3))) int32_t lds_i32;
 // (it is first read at B's phase 2, after the wait that ends phase 1).
 template <typename T, int kGrp>
 __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(const PrefillParams& p, int32_t* plan,
-                                                                             int h, lds_u8* tiles, lds_i32* nextq) {
+                                                                             int h0, lds_u8* tiles, lds_i32* nextq) {
   typedef typename Elem<T>::v8 V8;
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // 0..7
@@ -97,8 +104,21 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
   const int G = p.group;
   const int BMT = p.tile_tokens;  // 256 / G
   const int n_items = sload(plan, 0);
-  int* const ctr = plan + kPrefillPlanLineInts * (1 + h);
-  auto claim = [&]() { return __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  const int H = p.num_kv_heads;
+  auto claim = [&](int head) {
+    return __hip_atomic_fetch_add(plan + kPrefillPlanLineInts * (1 + head), 1, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+  };
+  // Thread 0: given the result r of a claim from `head`, claims from the
+  // following heads while r shows an exhausted queue; `head` ends at the
+  // head whose queue yielded r (r >= n_items: every queue is exhausted).
+  auto claim_on = [&](int r, int& head) {
+    for (int tried = 1; r >= n_items && tried < H; ++tried) {
+      head = head + 1 == H ? 0 : head + 1;
+      r = claim(head);
+    }
+    return r;
+  };
 
   // This lane's query row of every item: head g of the KV head, token rr of
   // the item's 256 / G tokens.
@@ -111,9 +131,10 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
   const uint32_t voff = (uint32_t)(((lane >> 2) * p.tok_stride + 8 * (lane & 3)) * (int64_t)sizeof(T));
   auto kbuf = [&](int x) { return tiles + (x % kPrefillPPBufs) * kPrefillTileBytes; };
   auto vbuf = [&](int x) { return tiles + (kPrefillPPBufs + x % kPrefillPPBufs) * kPrefillTileBytes; };
-  // This wave's page of K (group 0) or V (group 1) of global tile x.
-  auto copy_page = [&](int x, int page) __attribute__((always_inline)) {
-    const T* src = (const T*)(kGrp == 0 ? p.k_cache : p.v_cache) + h * kHeadDim;
+  // This wave's page of K (group 0) or V (group 1) of KV head `head`, global
+  // tile x.
+  auto copy_page = [&](int x, int page, int head) __attribute__((always_inline)) {
+    const T* src = (const T*)(kGrp == 0 ? p.k_cache : p.v_cache) + head * kHeadDim;
     lds_u8* buf = kGrp == 0 ? kbuf(x) : vbuf(x);
     dma16_x4_saddr(src + (int64_t)__builtin_amdgcn_readfirstlane(page) * p.page_stride, kGrp == 0 ? koff : voff,
                    (uint32_t)(uintptr_t)(buf + 4096 * slot));
@@ -133,13 +154,13 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
   };
 
   V8 qf[8];
-  // Query fragments of item `it` (rows past the sequence or the heads read
-  // zeros).
-  auto load_q = [&](const PrefillWork& it) __attribute__((always_inline)) {
+  // Query fragments of item `it` of KV head `kvh` (rows past the sequence or
+  // the heads read zeros).
+  auto load_q = [&](const PrefillWork& it, int kvh) __attribute__((always_inline)) {
     const int tq = it.t0 + rr;
     const bool ok = g < G && tq < it.q_len;
     const int row_tok = it.q0 + (ok ? tq : 0);
-    const int head = h * G + (g < G ? g : 0);
+    const int head = kvh * G + (g < G ? g : 0);
     const T* qp = (const T*)p.q + (int64_t)row_tok * p.q_tok_stride + (int64_t)head * p.q_head_stride;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) qf[kk] = ok ? ld16<V8>(qp + 8 * (2 * kk + hi)) : V8{};
@@ -180,22 +201,30 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
   };
 
   // ---- the first item ---------------------------------------------------------
-  if (tid == 0) nextq[0] = claim();
+  int claim_head = h0;  // thread 0: the head claimed from last
+  int claim_ret = 0;    // thread 0: the latest claim
+  if (tid == 0) {
+    nextq[0] = claim_on(claim(h0), claim_head);
+    nextq[3] = claim_head;
+  }
   __syncthreads();
   int idx = __builtin_amdgcn_readfirstlane(nextq[0]);
   if (idx >= n_items) return;  // uniform: nothing for this workgroup
+  int cur_h = __builtin_amdgcn_readfirstlane(nextq[3]);
   PrefillWork cur = plan_work_slot(plan, idx, slot);
-  int claim_ret = 0;  // thread 0: the latest claim
-  if (tid == 0) claim_ret = claim();
-  load_q(cur);
+  if (tid == 0) claim_ret = claim(claim_head);
+  load_q(cur, cur_h);
   if constexpr (kGrp == 0) {
-    copy_page(0, cur.pg0);
-    if (1 < cur.ntiles) copy_page(1, cur.pg1);
+    copy_page(0, cur.pg0, cur_h);
+    if (1 < cur.ntiles) copy_page(1, cur.pg1, cur_h);
   } else {
-    copy_page(0, cur.pg0);
+    copy_page(0, cur.pg0, cur_h);
   }
   __builtin_amdgcn_s_waitcnt(kVmcnt0);
-  if (tid == 0) nextq[1] = claim_ret;
+  if (tid == 0) {
+    nextq[1] = claim_on(claim_ret, claim_head);
+    nextq[2] = claim_head;
+  }
   phase_barrier();
   int G0 = 0;            // global index of the item's tile 0
   bool v0_done = true;   // V of the item's tile 0 is copied (group 1)
@@ -204,6 +233,7 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
   const std::false_type no;
   while (true) {
     const int nidx = __builtin_amdgcn_readfirstlane(nextq[1]);
+    const int nh = __builtin_amdgcn_readfirstlane(nextq[2]);  // B's KV head
     const bool has_next = nidx < n_items;
     const int n = cur.ntiles;
     const int full_tiles = cur.full_tiles;
@@ -223,7 +253,7 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
       if (has_next) nx = plan_work_slot(plan, nidx, slot);
     };
     if constexpr (kGrp == 1) {
-      if (!v0_done) copy_page(G0, cur.pg0);
+      if (!v0_done) copy_page(G0, cur.pg0, cur_h);
     }
     m = -INFINITY;
     l = 0.f;
@@ -362,24 +392,24 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
       int c = 0;
       if constexpr (kGrp == 0) {
         if (t + 2 < n) {
-          copy_page(G0 + t + 2, pg_next);
+          copy_page(G0 + t + 2, pg_next, cur_h);
           ++c;
         }
         if (has_next && t == max(n - 2, 1)) {
-          copy_page(G0 + n, nx.pg0);
+          copy_page(G0 + n, nx.pg0, nh);
           ++c;
         }
         if (has_next && t == max(n - 1, 1) && 1 < nx.ntiles) {
-          copy_page(G0 + n + 1, nx.pg1);
+          copy_page(G0 + n + 1, nx.pg1, nh);
           ++c;
         }
       } else {
         if (t + 1 < n) {
-          copy_page(G0 + t + 1, pg_next);
+          copy_page(G0 + t + 1, pg_next, cur_h);
           ++c;
         }
         if (has_next && n >= 2 && t == max(n - 1, 2)) {
-          copy_page(G0 + n, nx.pg0);
+          copy_page(G0 + n, nx.pg0, nh);
           ++c;
         }
       }
@@ -442,21 +472,24 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
     // has landed, and thread 0 publishes the claim.
     if constexpr (kGrp == 0) {
       if (has_next) {
-        load_q(nx);
-        if (tid == 0) claim_ret = claim();
+        load_q(nx, nh);
+        if (tid == 0) claim_ret = claim(claim_head);
       }
       issue(n);
       phase_m(n, no, yes);
       phase_barrier();
       __builtin_amdgcn_s_waitcnt(kVmcnt0);
-      if (tid == 0 && has_next) nextq[1] = claim_ret;
+      if (tid == 0 && has_next) {
+        nextq[1] = claim_on(claim_ret, claim_head);
+        nextq[2] = claim_head;
+      }
     } else {
       if (n == 1) load_next();
       issue(n);
-      if (has_next && n >= 2) load_q(nx);
+      if (has_next && n >= 2) load_q(nx, nh);
       phase_s(n - 1);
       phase_barrier();
-      if (has_next && n == 1) load_q(nx);
+      if (has_next && n == 1) load_q(nx, nh);
       phase_m(n, no, yes);
       __builtin_amdgcn_s_waitcnt(kVmcnt0);
     }
@@ -466,7 +499,7 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
     const float l_tot = pair_sum(l);
     if (row_ok) {
       const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-      T* op = (T*)p.out + (int64_t)(cur.q0 + tq) * p.out_tok_stride + (int64_t)(h * G + g) * p.out_head_stride;
+      T* op = (T*)p.out + (int64_t)(cur.q0 + tq) * p.out_tok_stride + (int64_t)(cur_h * G + g) * p.out_head_stride;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -483,6 +516,7 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
     G0 += n;
     v0_done = n >= 2;
     cur = nx;
+    cur_h = nh;
   }
 }
 
