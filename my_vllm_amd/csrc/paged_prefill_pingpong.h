@@ -65,10 +65,11 @@ typedef __attribute__((address_space(3))) int32_t lds_i32;
 // starts next.
 //
 // Claims: a workgroup of KV head h0 claims from h0's counter.  Once that
-// queue is exhausted it claims from the following heads' counters in turn
-// (their items then run here, with their own K/V and output columns), so
-// that the workgroups of a head served by a faster XCD take over the last
-// items of slower heads instead of idling.
+// queue is exhausted it reads every head's counter (one per lane of wave 0)
+// and claims from the head with the most items left (those items then run
+// here, with their own K/V and output columns), so that the workgroups of a
+// head served by a faster XCD take over the last items of slower heads
+// instead of idling.
 //
 // Tiles are numbered across items: the tiles of an item that starts at
 // global tile G0 are G0 .. G0 + n - 1, and global tile x uses buffer
@@ -109,13 +110,35 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
     return __hip_atomic_fetch_add(plan + kPrefillPlanLineInts * (1 + head), 1, __ATOMIC_RELAXED,
                                   __HIP_MEMORY_SCOPE_AGENT);
   };
-  // Thread 0: given the result r of a claim from `head`, claims from the
-  // following heads while r shows an exhausted queue; `head` ends at the
-  // head whose queue yielded r (r >= n_items: every queue is exhausted).
-  auto claim_on = [&](int r, int& head) {
-    for (int tried = 1; r >= n_items && tried < H; ++tried) {
-      head = head + 1 == H ? 0 : head + 1;
-      r = claim(head);
+  // Wave 0 (all lanes): given r, lane 0's claim from `head`, and while r
+  // shows an exhausted queue, reads every head's counter at once (one head
+  // per lane) and claims from the head with the most items left; `head`
+  // ends at the head whose queue yielded the returned index (>= n_items:
+  // nothing left, or four claims lost to other workgroups).
+  auto claim_on = [&](int r0, int& head) {
+    int r = __builtin_amdgcn_readfirstlane(r0);
+    for (int round = 0; r >= n_items && round < 4; ++round) {
+      int best_left = 0, best_h = 0;
+      for (int base = 0; base < H; base += 64) {
+        const int hh = base + lane;
+        int left = 0;
+        if (hh < H)
+          left = n_items - __hip_atomic_load(plan + kPrefillPlanLineInts * (1 + hh), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        int mx = left;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) mx = max(mx, __shfl_xor(mx, off));
+        mx = __builtin_amdgcn_readfirstlane(mx);
+        if (mx > best_left) {
+          best_left = mx;
+          best_h = base + (int)__builtin_ctzll(__builtin_amdgcn_ballot_w64(left == mx));
+        }
+      }
+      if (best_left <= 0) break;
+      head = best_h;
+      int rr = 0;
+      if (lane == 0) rr = claim(head);
+      r = __builtin_amdgcn_readfirstlane(rr);
     }
     return r;
   };
@@ -201,11 +224,16 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
   };
 
   // ---- the first item ---------------------------------------------------------
-  int claim_head = h0;  // thread 0: the head claimed from last
+  int claim_head = h0;  // wave 0: the head claimed from last
   int claim_ret = 0;    // thread 0: the latest claim
-  if (tid == 0) {
-    nextq[0] = claim_on(claim(h0), claim_head);
-    nextq[3] = claim_head;
+  if (w == 0) {
+    int r = 0;
+    if (lane == 0) r = claim(h0);
+    r = claim_on(r, claim_head);
+    if (lane == 0) {
+      nextq[0] = r;
+      nextq[3] = claim_head;
+    }
   }
   __syncthreads();
   int idx = __builtin_amdgcn_readfirstlane(nextq[0]);
@@ -221,9 +249,12 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
     copy_page(0, cur.pg0, cur_h);
   }
   __builtin_amdgcn_s_waitcnt(kVmcnt0);
-  if (tid == 0) {
-    nextq[1] = claim_on(claim_ret, claim_head);
-    nextq[2] = claim_head;
+  if (w == 0) {
+    const int r = claim_on(claim_ret, claim_head);
+    if (lane == 0) {
+      nextq[1] = r;
+      nextq[2] = claim_head;
+    }
   }
   phase_barrier();
   int G0 = 0;            // global index of the item's tile 0
@@ -479,9 +510,12 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
       phase_m(n, no, yes);
       phase_barrier();
       __builtin_amdgcn_s_waitcnt(kVmcnt0);
-      if (tid == 0 && has_next) {
-        nextq[1] = claim_on(claim_ret, claim_head);
-        nextq[2] = claim_head;
+      if (w == 0 && has_next) {
+        const int r = claim_on(claim_ret, claim_head);
+        if (lane == 0) {
+          nextq[1] = r;
+          nextq[2] = claim_head;
+        }
       }
     } else {
       if (n == 1) load_next();
