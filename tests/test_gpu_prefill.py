@@ -76,7 +76,9 @@ def test_qwen3_8b_prefill_with_prefix_configuration(gpu):
     assert_attention_close(out.cpu()[rows], exp)
 
 
-@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (32, 8), (64, 8), (128, 8), (12, 4), (16, 1)])
+# (80, 80): more KV heads than a wavefront has lanes, so a workgroup whose
+# own queue is exhausted reads the other heads' claim counters in two rounds.
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (32, 8), (64, 8), (128, 8), (12, 4), (16, 1), (80, 80)])
 def test_gqa_ratios(gpu, hq, hkv):
     q = [1, 37, 130, 64]
     kv = [1, 37 + 16 * 3, 130 + 5, 64 + 200]
@@ -273,3 +275,16 @@ def test_more_sequences_than_the_planner_sorts(gpu):
     assert_attention_close(out.cpu()[rows], exp)
     # Rows of every sequence are written (no NaN from the backend's buffer).
     assert bool(torch.isfinite(out.float()).all())
+
+
+def test_tiles_of_other_kv_heads_run_with_their_own_heads(gpu):
+    # Many one-tile items and more workgroups than one head's items: the
+    # workgroups whose own queue empties first take other heads' tiles, which
+    # must read that head's K/V and write that head's output columns.
+    q = [3, 1, 2, 4, 1, 5, 2, 1, 3, 2, 6, 1]
+    kv = [x + 16 * (i % 5) + 7 for i, x in enumerate(q)]
+    batch = make_paged_batch(149, q, kv, len(q), 32, 8)
+    for _ in range(3):
+        out, _ = run_backend(batch, gpu)
+        assert_attention_close(out, expected(batch))
+
