@@ -205,9 +205,13 @@ def make_decode_plan(
 # Workgroups of a piece-list decode launch fill 8 wave slots per CU (the
 # kernel's occupancy is 2 wavefronts per SIMD).
 _LISTED_WAVES_PER_CU = 8
-# Piece lists (an equal share of pages per wavefront, no claims) up to this
-# many K/V bytes per launch; larger batches use claims, whose dynamic
-# balance absorbs the uneven per-CU bandwidth of a long launch.
+# Piece lists (an equal share of pages per wavefront, no claims) at every
+# size when a workgroup holds all 8 KV heads of its range (one CU streams
+# every head of the same pages): measured as fast as claims or faster from
+# 1.3 to 11.2 GB of K/V (3.21 GB, 16 sequences of 32K-64K tokens: 5.6 against
+# 4.95 TB/s; 4.6 GB, 256 sequences of 512-8192: 5.75 against 5.4 TB/s).  Other
+# head counts use them up to this many K/V bytes per launch (at 4 KV heads
+# and 4.8 GB, claims measured 2% faster); larger batches use claims.
 _LISTED_MAX_BYTES = 2 << 30
 
 
@@ -218,6 +222,8 @@ def decode_schedule(total_pages: int, num_kv_heads: int, elem_bytes: int = 2, fo
         if forced not in ("listed", "claims"):
             raise ValueError("decode schedule must be 'listed' or 'claims'")
         return forced
+    if num_kv_heads == _LISTED_WAVES_PER_CU:
+        return "listed"
     kv_bytes = total_pages * PAGE_SIZE * num_kv_heads * HEAD_DIM * elem_bytes * 2
     return "listed" if kv_bytes <= _LISTED_MAX_BYTES else "claims"
 

@@ -3,9 +3,9 @@
 
 Decode: 64 Q / 8 KV heads, head_dim 128, bf16, 16-token pages, batch 128 with
 contexts uniform in [8192, 32768] (seed 4) over randomly permuted pages: one
-layer's K/V, about 10.7 GB, drawn on the GPU.  This batch is above the
-piece-list limit, so the backend plans the claim schedule; the piece-list
-schedule is forced on the same batch as well.  The shortest, the longest and
+layer's K/V, about 11.2 GB, drawn on the GPU.  With 8 KV heads the backend
+plans piece lists at any size; the claim schedule is forced on the same
+batch as well.  The shortest, the longest and
 two random sequences are checked against the fp32 oracle on the host (their
 pages gathered from the device), and every output row must be finite.
 
@@ -51,18 +51,18 @@ def _host_expected(batch, seqs):
     return torch.cat(rows)
 
 
-@pytest.mark.parametrize("schedule", ["default", "listed"])
+@pytest.mark.parametrize("schedule", ["default", "claims"])
 def test_qwen3_32b_long_decode_configuration(gpu, long_batch, monkeypatch, schedule):
     batch = long_batch
-    if schedule == "listed":
-        set_decode_planning(monkeypatch, schedule="listed")
+    if schedule == "claims":
+        set_decode_planning(monkeypatch, schedule="claims")
     backend = MI355XAttentionBackend(64, 8, 128, 16, torch.bfloat16)
     plan = backend.build_plan(batch.common)
     assert plan.route is AttentionRoute.DECODE
     if schedule == "default":
-        assert plan.metadata.decode_wave_extra is None, "a >2 GB batch plans the claim schedule"
+        assert plan.metadata.decode_wave_extra is not None, "8 KV heads plan piece lists at any size"
     else:
-        assert plan.metadata.decode_wave_extra is not None
+        assert plan.metadata.decode_wave_extra is None
     empty = batch.q.new_empty((0, 8, 128))
     out = backend.forward(batch.q, empty, empty, batch.k_cache, batch.v_cache, plan)
     torch.cuda.synchronize()

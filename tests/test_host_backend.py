@@ -18,6 +18,7 @@ from my_vllm_amd.attention_backend import (
     MI355XAttentionBackend,
     MI355XAttentionMetadata,
     MI355XSplitAttentionBackend,
+    decode_schedule,
     integrate,
     make_decode_plan,
     make_decode_plan_listed,
@@ -356,6 +357,24 @@ def test_listed_decode_plan_tiles_every_wavefront_range(seed):
     counts = rng.integers(1, 400, size=int(rng.integers(1, 40))).tolist()
     _check_listed_plan(counts, int(rng.choice([1, 2, 3, 4, 8])), int(rng.integers(1, 3000)),
                        int(rng.choice([1, 3, 17, 128])))
+
+
+def test_decode_schedule_by_head_count_and_size():
+    # Pages of 16 tokens x 128 dims x bf16, K and V: 8 KiB per page and KV head.
+    pages_of = lambda gib, hkv: int(gib * (1 << 30)) // (8192 * hkv)
+    # Eight KV heads fill a workgroup: piece lists at every size.
+    assert decode_schedule(pages_of(0.5, 8), 8) == "listed"
+    assert decode_schedule(pages_of(11.2, 8), 8) == "listed"
+    # Other head counts: piece lists up to 2 GiB of K/V, claims above.
+    assert decode_schedule(pages_of(2.0, 4), 4) == "listed"
+    assert decode_schedule(pages_of(2.0, 4) + 1, 4) == "claims"
+    assert decode_schedule(pages_of(3.0, 16), 16) == "claims"
+    assert decode_schedule(pages_of(1.0, 1), 1) == "listed"
+    # A backend's override picks either one.
+    assert decode_schedule(pages_of(11.2, 8), 8, forced="claims") == "claims"
+    assert decode_schedule(10, 4, forced="listed") == "listed"
+    with pytest.raises(ValueError):
+        decode_schedule(10, 8, forced="static")
 
 
 def test_listed_decode_plan_edges():
