@@ -60,6 +60,7 @@ struct PrefillParams {
   int group;
   int tile_tokens;  // BMT = 128 / group (rounded down)
   float scale_log2;
+  int out16;  // out and its strides are 16-byte aligned (16-byte output stores)
 };
 
 // LDS tile layouts.  A 64-key x 128-d tile is 16 blocks of 1 KB, block

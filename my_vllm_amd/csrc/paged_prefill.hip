@@ -375,6 +375,7 @@ int fill_prefill_params(PrefillParams& p, const void* q, int64_t q_token_stride,
   p.group = group;
   p.tile_tokens = kPrefillRows / group;
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
+  p.out16 = ((uint64_t)(uintptr_t)out | (uint64_t)(out_token_stride * 2) | (uint64_t)(out_head_stride * 2)) % 16 == 0;
   return 0;
 }
 

@@ -288,3 +288,27 @@ def test_tiles_of_other_kv_heads_run_with_their_own_heads(gpu):
         out, _ = run_backend(batch, gpu)
         assert_attention_close(out, expected(batch))
 
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_output_only_8_byte_aligned_matches_aligned(gpu, dtype):
+    # The kernel stores 16 bytes per lane when the output and its strides are
+    # 16-byte aligned and 8 bytes otherwise; an output view 8 bytes past an
+    # aligned buffer takes the second path and must give the same bits.
+    q = [300, 37, 130, 64, 1]
+    kv = [300 + 48, 37, 130 + 16, 64, 90]
+    batch = make_paged_batch(151, q, kv, len(q), 32, 8, dtype=dtype)
+    common, qd, kc, vc = to_device(batch, gpu)
+    tile = ops.PREFILL_STREAM_ROWS // 4
+    n_tiles = len(_expected_tiles(q, kv, tile))
+    ws = torch.empty(ops.prefill_workspace_bytes(n_tiles), dtype=torch.uint8, device=gpu)
+    outs = []
+    for shift in (0, 4):
+        flat = torch.full((qd.numel() + 8,), float("nan"), dtype=dtype, device=gpu)
+        out = flat[shift:shift + qd.numel()].view(qd.shape)
+        assert (out.data_ptr() % 16 == 0) == (shift == 0)
+        ops.paged_prefill(qd, kc, vc, common.block_tables, common.seq_lens, common.query_start_loc, len(q), n_tiles,
+                          ws, out, 128 ** -0.5)
+        outs.append(out.clone())
+    assert torch.equal(outs[0], outs[1])
+    assert_attention_close(outs[0].cpu(), expected(batch))
