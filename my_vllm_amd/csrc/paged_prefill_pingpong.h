@@ -76,8 +76,10 @@ typedef __attribute__((address_space(3))) int32_t lds_i32;
 // x % kPrefillPPBufs, so the copy stream runs on from one item into the
 // next.  While item A runs, its successor B is already claimed (its index
 // is read at A's start) and A's phases prepare B:
-//   * at A's first S phase each wave loads B's plan record (scalar loads,
-//     in an S phase so that no LDS wait waits behind them);
+//   * each wave loads B's plan record at the end of its group's first M
+//     phase (phase 0 for group 0, 1 for group 1), after its LDS reads, where
+//     the group would wait for the other at the barrier anyway, and B's
+//     tile-2 page in A's last phases;
 //   * group 0 copies K(B, 0) at phase 2 max(n - 2, 1) and K(B, 1) at phase
 //     2 max(n - 1, 1), group 1 copies V(B, 0) at phase 2 max(n - 1, 2) when
 //     that phase exists (n >= 2); each is the earliest even phase at which
@@ -223,6 +225,13 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
     else __builtin_amdgcn_s_waitcnt(kVmcnt0);
   };
 
+  // Page id of tile `tile` of item `it` at this wave's page slot.
+  auto page_of_item = [&](const PrefillWork& it, int tile) {
+    const int32_t* btp = p.block_tables + (int64_t)it.s * p.bt_stride;
+    const int pg = sload(btp, min(tile * (kPrefillKeys / kPageSize) + slot, it.npages - 1));
+    return (pg >= 0 && pg < p.num_pages) ? pg : 0;
+  };
+
   // ---- the first item ---------------------------------------------------------
   int claim_head = h0;  // wave 0: the head claimed from last
   int claim_ret = 0;    // thread 0: the latest claim
@@ -240,6 +249,9 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
   if (idx >= n_items) return;  // uniform: nothing for this workgroup
   int cur_h = __builtin_amdgcn_readfirstlane(nextq[3]);
   PrefillWork cur = plan_work_slot(plan, idx, slot);
+  // The page of the item's tile 2, which the item's first copies need; for
+  // later items it is loaded during the item before (see below).
+  int pg2_next = page_of_item(cur, 2);
   if (tid == 0) claim_ret = claim(claim_head);
   load_q(cur, cur_h);
   if constexpr (kGrp == 0) {
@@ -272,12 +284,7 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
     const int tq = cur.t0 + rr;
     const bool row_ok = g < G && tq < cur.q_len;
     const int pos = row_ok ? kv - cur.q_len + tq : -1;  // keys j <= pos are visible
-    const int32_t* bt = p.block_tables + (int64_t)cur.s * p.bt_stride;
-    const int npages = cur.npages;
-    auto page_of = [&](int tile) {
-      const int pg = sload(bt, min(tile * (kPrefillKeys / kPageSize) + slot, npages - 1));
-      return (pg >= 0 && pg < p.num_pages) ? pg : 0;
-    };
+    auto page_of = [&](int tile) { return page_of_item(cur, tile); };
     PrefillWork nx;  // B's record, loaded at this item's first S phase
     nx.ntiles = 0;
     auto load_next = [&]() __attribute__((always_inline)) {
@@ -468,18 +475,22 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
       }
     };
     // Phases 0 and 1.
-    pg_next = kGrp == 0 ? page_of(2) : __builtin_amdgcn_readfirstlane(cur.pg1);
+    pg_next = kGrp == 0 ? pg2_next : __builtin_amdgcn_readfirstlane(cur.pg1);
     int c = issue(0);
+    // B's record (and group 0's tile-3 page) are loaded at the end of the
+    // group's phase-0 / phase-1 M phase, where it waits for the other group
+    // anyway (its LDS reads are done, so nothing waits behind the loads).
     if constexpr (kGrp == 0) {
       phase_m(0, yes, no);
-      phase_barrier();
       load_next();
       pg_next = page_of(3);
+      phase_barrier();
       phase_s(0);
     } else {
-      pg_next = page_of(2);
+      pg_next = pg2_next;
       phase_barrier();
       phase_m(0, yes, no);
+      load_next();
     }
     end_odd_phase(0, c);
     // Phases 2t and 2t+1, t = 1 .. n-1.
@@ -491,7 +502,6 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
         pg_next = page_of(t + 3);
         phase_s(t);
       } else {
-        if (t == 1) load_next();
         pg_next = page_of(t + 2);
         phase_s(t - 1);
         phase_barrier();
@@ -509,6 +519,8 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
       issue(n);
       phase_m(n, no, yes);
       phase_barrier();
+      // B's tile-2 page, loaded while this group waits for group 1's M(n).
+      if (has_next) pg2_next = page_of_item(nx, 2);
       __builtin_amdgcn_s_waitcnt(kVmcnt0);
       if (w == 0 && has_next) {
         const int r = claim_on(claim_ret, claim_head);
@@ -518,9 +530,10 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
         }
       }
     } else {
-      if (n == 1) load_next();
       issue(n);
       if (has_next && n >= 2) load_q(nx, nh);
+      // B's tile-2 page, in an S phase (no LDS read waits behind the load).
+      if (has_next) pg2_next = page_of_item(nx, 2);
       phase_s(n - 1);
       phase_barrier();
       if (has_next && n == 1) load_q(nx, nh);
