@@ -89,6 +89,50 @@ __device__ inline float pair_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// O^T / l of a lane's query row to out (op: the row's first column).  Lane
+// (row, hi) holds d = 32 dt + 8 bk + 4 hi + 0..3 in o[dt][4 bk ..].  With a
+// 16-byte aligned output (p.out16) one v_permlane32_swap per word pair gives
+// lane hi = 0 d = 32 dt + 16 b + 0..7 and lane hi = 1 d = 32 dt + 16 b +
+// 8..15 (both lanes of a pair hold the same row): 16 contiguous bytes per
+// lane, half the store instructions and half the partial cache-line writes
+// of 8-byte stores.  Every lane of the wave calls it.
+template <typename T>
+__device__ inline void store_rows(const PrefillParams& p, T* op, const f32x16 (&o)[4], float inv, bool row_ok) {
+  const int hi = (int)(threadIdx.x & 63) >> 5;
+  if (p.out16) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        typename Elem<T>::v4 lo, up;  // d chunks bk = 2b and 2b + 1
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lo[e] = (T)(o[dt][8 * b + e] * inv);
+          up[e] = (T)(o[dt][8 * b + 4 + e] * inv);
+        }
+        const u32x2 lw = __builtin_bit_cast(u32x2, lo), uw = __builtin_bit_cast(u32x2, up);
+        u32x4 wv;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const auto r = __builtin_amdgcn_permlane32_swap(lw[k], uw[k], false, false);
+          wv[k] = r[0];
+          wv[2 + k] = r[1];
+        }
+        if (row_ok) *reinterpret_cast<u32x4*>(op + 32 * dt + 16 * b + 8 * hi) = wv;
+      }
+  } else if (row_ok) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int bk = 0; bk < 4; ++bk) {
+        typename Elem<T>::v4 wv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wv[e] = (T)(o[dt][4 * bk + e] * inv);
+        *reinterpret_cast<typename Elem<T>::v4*>(op + 32 * dt + 8 * bk + 4 * hi) = wv;
+      }
+  }
+}
+
 // Two probabilities rounded to the storage type and packed into one word.
 template <typename T>
 struct PackedPair;
@@ -401,18 +445,9 @@ __device__ __attribute__((always_inline)) inline void prefill_core(const Prefill
 
   // Epilogue: O^T / l -> out[token][head][d].
   const float l_tot = pair_sum(l);
-  if (!row_ok) return;
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
   T* op = (T*)p.out + (int64_t)(q0 + tq) * p.out_tok_stride + (int64_t)(h * G + g) * p.out_head_stride;
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-    for (int bk = 0; bk < 4; ++bk) {
-      typename Elem<T>::v4 wv;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) wv[e] = (T)(o[dt][4 * bk + e] * inv);
-      *reinterpret_cast<typename Elem<T>::v4*>(op + 32 * dt + 8 * bk + 4 * hi) = wv;
-    }
+  store_rows<T>(p, op, o, inv, row_ok);
 }
 
 
