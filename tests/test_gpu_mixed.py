@@ -251,3 +251,32 @@ def test_mixed_untrusted_metadata_matches_trusted(gpu):
     b, plan = run_backend(batch, gpu, trusted=False)
     assert plan.route is AttentionRoute.MIXED_UNIFIED
     assert torch.equal(a, b)
+
+
+def test_mixed_output_only_8_byte_aligned_matches_aligned(gpu):
+    # The single launch's prefill rows are stored 16 bytes per lane when the
+    # output and its strides are 16-byte aligned and 8 bytes otherwise; an
+    # output view 8 bytes past an aligned buffer takes the second path and
+    # must give the same bits (its decode rows as well).
+    from my_vllm_amd import ops
+    from my_vllm_amd.attention_backend import MI355XAttentionBackend
+    from tests.test_gpu_prefill import to_device
+
+    batch = make_paged_batch(157, [70, 300, 1, 1, 1], [70, 900, 40, 700, 2000], 2, 32, 8)
+    backend = MI355XAttentionBackend(32, 8, 128, 16, torch.bfloat16)
+    common, qd, kc, vc = to_device(batch, gpu)
+    plan = backend.build_plan(common)
+    assert plan.route is AttentionRoute.MIXED_UNIFIED
+    md = plan.metadata
+    ws = backend._get_workspace(ops.decode_workspace_bytes(md.num_decode_part_slots, 8, 4), qd.device)
+    outs = []
+    for shift in (0, 4):
+        flat = torch.full((qd.numel() + 8,), float("nan"), dtype=qd.dtype, device=gpu)
+        out = flat[shift:shift + qd.numel()].view(qd.shape)
+        assert (out.data_ptr() % 16 == 0) == (shift == 0)
+        ops.paged_mixed(qd, kc, vc, md.block_tables, md.seq_lens, md.query_start_loc, common.num_prefill_seqs,
+                        md.mixed_prefill_max_tiles, md.decode_items, md.num_decode_items, md.num_decode_waves,
+                        md.num_decode_part_slots, out, ws, backend.softmax_scale)
+        outs.append(out.clone())
+    assert torch.equal(outs[0], outs[1])
+    assert_attention_close(outs[0], expected(batch))
