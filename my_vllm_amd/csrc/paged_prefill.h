@@ -133,6 +133,56 @@ __device__ inline void store_rows(const PrefillParams& p, T* op, const f32x16 (&
   }
 }
 
+// The same rows written as whole cache lines: the wavefront's 32 rows go
+// through a 4 KB LDS area `stage`, 64 columns at a time, and come back so
+// that each 16-byte store instruction covers 8 rows x 128 contiguous bytes.
+// The stores are non-temporal: the output is not read again by the launch,
+// and written as ordinary stores its lines displace K/V lines that other
+// workgroups still read from L2.  rowp[j] and rok[j] are the output address
+// (column 8 * (lane % 8)) and validity of wavefront row 8j + lane / 8.  The
+// stage rows are 128 bytes, their 16-byte chunks XOR-swizzled by row / 2, so
+// that the row-per-lane writes and the chunk-per-lane reads both cover all
+// banks.  Requires 16-byte aligned output rows (PrefillParams::out16).
+template <typename T>
+__device__ inline void store_rows_staged(lds_u8* stage, const f32x16 (&o)[4], float inv, T* const (&rowp)[4],
+                                         const bool (&rok)[4]) {
+  const int lane = (int)(threadIdx.x & 63);
+  const int ln = lane & 31, hi = lane >> 5;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+#pragma unroll
+    for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const int dt = 2 * half + dd;
+        typename Elem<T>::v4 lo, up;  // this lane's columns 32dt + 16b + 4hi + (0..3) and + 8
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lo[e] = (T)(o[dt][8 * b + e] * inv);
+          up[e] = (T)(o[dt][8 * b + 4 + e] * inv);
+        }
+        const u32x2 lw = __builtin_bit_cast(u32x2, lo), uw = __builtin_bit_cast(u32x2, up);
+        u32x4 wv;  // columns 32dt + 16b + 8hi .. + 7
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const auto r = __builtin_amdgcn_permlane32_swap(lw[k], uw[k], false, false);
+          wv[k] = r[0];
+          wv[2 + k] = r[1];
+        }
+        const int c = 4 * dd + 2 * b + hi;  // 16-byte chunk of the 64 columns
+        lds_st16<u32x4>(stage + ln * 128 + ((c ^ ((ln >> 1) & 7)) << 4), wv);
+      }
+    wave_lds_fence();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = 8 * j + (lane >> 3), c = lane & 7;
+      const u32x4 v = lds_ld16<u32x4>(stage + row * 128 + ((c ^ ((row >> 1) & 7)) << 4));
+      if (rok[j]) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(rowp[j] + 64 * half));
+    }
+    wave_lds_fence();
+  }
+}
+
 // Two probabilities rounded to the storage type and packed into one word.
 template <typename T>
 struct PackedPair;

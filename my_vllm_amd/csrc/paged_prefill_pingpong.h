@@ -346,16 +346,32 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
       if (t >= full_tiles) {
         // Key t*64 + 32*mt + 8*(i/4) + 4*hi + i%4 is visible when
         // 32*mt + 8*(i/4) + i%4 <= lim.  lim and S pass through an empty asm
-        // statement so that the compares and selects stay inside this branch:
-        // hoisted, they would run on every tile and hold 32 compare masks in
-        // scalar registers.
+        // statement so that the masking stays inside this branch.  Bit k of
+        // vis[mt] says whether offset 32*mt + k is visible; each element is
+        // then a bit extract and a bit select on vector registers.  (Written
+        // as compares and selects, the compiler computes all 32 compare masks
+        // first and keeps them in scalar registers, which pushed the loop's
+        // other scalar state out to VGPR lanes: about 20 v_readlane restores
+        // per tile in every phase that issues a copy.)
         int lim = pos - t * kPrefillKeys - 4 * hi;
         asm volatile("" : "+v"(lim), "+v"(st[0]), "+v"(st[1]));
+        uint32_t vis[2];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          const int bl = lim - 32 * mt;
+          vis[mt] = bl < 0 ? 0u : bl >= 31 ? ~0u : (2u << bl) - 1u;
+        }
+        const uint32_t ninf = 0xff800000u;  // -inf
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-          for (int i = 0; i < 16; ++i)
-            if (32 * mt + 8 * (i >> 2) + (i & 3) > lim) st[mt][i] = -INFINITY;
+          for (int i = 0; i < 16; ++i) {
+            int sel;  // all ones when the key is visible
+            uint32_t x = __float_as_uint(st[mt][i]);
+            asm volatile("v_bfe_i32 %0, %1, %2, 1" : "=v"(sel) : "v"(vis[mt]), "i"(8 * (i >> 2) + (i & 3)));
+            asm volatile("v_bfi_b32 %0, %1, %2, %3" : "=v"(x) : "v"(sel), "v"(x), "s"(ninf));
+            st[mt][i] = __uint_as_float(x);
+          }
       }
       if (t > 0) {
         const float m_fast = (m == -INFINITY) ? 0.f : m;
@@ -545,8 +561,32 @@ __device__ __attribute__((always_inline)) inline void prefill_items_pingpong(con
     // Epilogue: O^T / l -> out[token][head][d].
     const float l_tot = pair_sum(l);
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-    T* op = (T*)p.out + (int64_t)(cur.q0 + tq) * p.out_tok_stride + (int64_t)(cur_h * G + g) * p.out_head_stride;
-    store_rows<T>(p, op, o, inv, row_ok);
+    if (p.out16) {
+      // Staged in this wave's page slot of the K buffer (group 0) or V
+      // buffer (group 1) of the item's last tile: the K buffer is next
+      // written by this wave's own copy at the next item's phase 0, the V
+      // buffer at its phase 2.
+      lds_u8* stage = (kGrp == 0 ? kbuf(G0 + n - 1) : vbuf(G0 + n - 1)) + 4096 * slot;
+      // Row 8j + lane / 8 of the wave: head g0 + (0..2), token rr0 + ...
+      // (256 / G >= 16 tokens per head, so 32 rows span at most 3 heads).
+      const int g0 = (32 * w) / BMT, rr0 = (32 * w) % BMT;
+      T* rowp[4];
+      bool rok[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        int rj = rr0 + 8 * j + (lane >> 3), gj = g0;
+        if (rj >= BMT) rj -= BMT, ++gj;
+        if (rj >= BMT) rj -= BMT, ++gj;
+        const int tj = cur.t0 + rj;
+        rok[j] = gj < G && tj < cur.q_len;
+        rowp[j] = (T*)p.out + (int64_t)(cur.q0 + (rok[j] ? tj : 0)) * p.out_tok_stride +
+                  (int64_t)(cur_h * G + (rok[j] ? gj : 0)) * p.out_head_stride + 8 * (lane & 7);
+      }
+      store_rows_staged<T>(stage, o, inv, rowp, rok);
+    } else {
+      T* op = (T*)p.out + (int64_t)(cur.q0 + tq) * p.out_tok_stride + (int64_t)(cur_h * G + g) * p.out_head_stride;
+      store_rows<T>(p, op, o, inv, row_ok);
+    }
     if (!has_next) return;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{};
