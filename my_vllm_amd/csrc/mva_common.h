@@ -98,26 +98,27 @@ __device__ inline s16x4 lds_ld_tr16(const lds_u8* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
 }
 
-// Eight ds_read_b64_tr_b16 at byte offsets base + 512*i (i = 0..7), then
-// lgkmcnt(0).  Issued as one asm block: the compiler cannot see that these
-// reads do not alias in-flight global_load_lds writes to another LDS buffer
-// and would otherwise wait for every outstanding DMA before each read.
-// Callers order the block after the waits that make `base` valid.
-__device__ inline void lds_ld_tr16_x8_stride512(const lds_u8* base, s16x4 (&out)[8]) {
-  const uint32_t a = (uint32_t)(uintptr_t)base;
+// Eight ds_read_b64_tr_b16: i = 0..3 at b[i], i = 4..7 at b[i - 4] + 2048,
+// then lgkmcnt(0).  Issued as one asm block: the compiler cannot see that
+// these reads do not alias in-flight global_load_lds writes to another LDS
+// buffer and would otherwise wait for every outstanding DMA before each
+// read.  Callers order the block after the waits that make the bases valid.
+__device__ inline void lds_ld_tr16_x8_4base(const lds_u8* b0, const lds_u8* b1, const lds_u8* b2, const lds_u8* b3,
+                                             s16x4 (&out)[8]) {
   asm volatile(
       "ds_read_b64_tr_b16 %0, %8\n"
-      "ds_read_b64_tr_b16 %1, %8 offset:512\n"
-      "ds_read_b64_tr_b16 %2, %8 offset:1024\n"
-      "ds_read_b64_tr_b16 %3, %8 offset:1536\n"
+      "ds_read_b64_tr_b16 %1, %9\n"
+      "ds_read_b64_tr_b16 %2, %10\n"
+      "ds_read_b64_tr_b16 %3, %11\n"
       "ds_read_b64_tr_b16 %4, %8 offset:2048\n"
-      "ds_read_b64_tr_b16 %5, %8 offset:2560\n"
-      "ds_read_b64_tr_b16 %6, %8 offset:3072\n"
-      "ds_read_b64_tr_b16 %7, %8 offset:3584\n"
+      "ds_read_b64_tr_b16 %5, %9 offset:2048\n"
+      "ds_read_b64_tr_b16 %6, %10 offset:2048\n"
+      "ds_read_b64_tr_b16 %7, %11 offset:2048\n"
       "s_waitcnt lgkmcnt(0)"
       : "=&v"(out[0]), "=&v"(out[1]), "=&v"(out[2]), "=&v"(out[3]), "=&v"(out[4]), "=&v"(out[5]),
         "=&v"(out[6]), "=&v"(out[7])
-      : "v"(a)
+      : "v"((uint32_t)(uintptr_t)b0), "v"((uint32_t)(uintptr_t)b1), "v"((uint32_t)(uintptr_t)b2),
+        "v"((uint32_t)(uintptr_t)b3)
       : "memory");
 }
 

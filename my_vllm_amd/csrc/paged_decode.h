@@ -32,12 +32,13 @@
 //    heads: S^T[token, g] = K[token, :] . Q[g, :].
 //  * A tile is one 16-token page of one KV head (4 KB of K, 4 KB of V).  Both
 //    go from HBM straight into LDS with global_load_lds (16 bytes per lane,
-//    no registers), double-buffered, so a wavefront never carries pending
-//    loads in registers.
-//  * S^T (16x16x32 MFMA): A = K fragments read from a chunk-major LDS page
+//    8 tokens x 128 contiguous bytes per instruction, no registers),
+//    double-buffered, so a wavefront never carries pending loads in
+//    registers.
+//  * S^T (16x16x32 MFMA): A = K fragments read from the swizzled LDS page
 //    (lane = token), B = Q held in registers.  PV (16x16x16 MFMA):
 //    O^T[d, g] += V^T[d, t] P^T[t, g], A = V^T read with ds_read_b64_tr_b16
-//    from a chunk-major LDS page; B = P^T is exactly the C layout of S^T, so
+//    from the swizzled LDS page; B = P^T is exactly the C layout of S^T, so
 //    no shuffle is needed.
 //  * Online softmax in the log2 domain, fp32 accumulators, P rounded to the
 //    storage type for the PV MFMA; the O rescale is skipped unless the
@@ -164,12 +165,16 @@ __device__ inline int sload(const int32_t* base, int64_t idx) { return ((const_i
 //   * if kDma: the 8 DMAs of one page of one KV head (4 to lds_v, 4 to
 //     lds_k, 1 KB each), then s_waitcnt vmcnt(8), which retires everything
 //     above and the previous page; otherwise s_waitcnt vmcnt(0).
-// Page layout in LDS: K at lds_k and V at lds_v are both chunk-major (byte
-// chunk*256 + token*16).  DMA i reads, per lane, 16 bytes at v_src/k_src +
-// 64*i, where the caller's lane address is token lane%16, d-chunk lane/16,
-// so DMA i holds d-chunks 4i..4i+3 of all 16 tokens.  The K A-operand read
-// (16 tokens at one chunk) and the V transposed read (4 tokens x 2 chunks
-// per 16-lane group) both cover whole 256-byte bank rows.
+// Page layout in LDS (K at lds_k, V at lds_v, 4 KB each): 16-byte chunk ch
+// (of 16 per token) of token t at byte
+//   (2 * (ch / 8) + t / 8) * 1024 + (t % 8) * 128 + ((ch % 8) ^ swz(t)) * 16,
+// swz(t) = 2 * ((t / 2) % 4) + (t / 8) % 2: each 1 KB block holds 8 tokens x
+// 128 contiguous cache bytes, so every DMA reads whole 128-byte lines.  The
+// caller's lane addresses src0 (tokens 0-7) and src1 (tokens 8-15) point at
+// token lane/8 (+8), chunk (lane%8) ^ swz; DMA i reads src{i%2} + 128*(i/2)
+// and fills block i.  The swizzle keeps the K A-operand reads (16 tokens at
+// one chunk per 16 lanes) and the V transposed reads (8 tokens x 2 chunks per
+// 32 lanes) free of bank conflicts.
 // `loading` and `claiming` are wave-uniform.  Outputs not issued keep their previous
 // contents (claim: unspecified).
 struct DecodeStepIo {
@@ -180,16 +185,19 @@ struct DecodeStepIo {
 };
 
 template <bool kDma>
-__device__ inline void decode_step(DecodeStepIo& io, int loading, int claiming, int* claim_ptr, const int32_t* bt0, const int32_t* bt1, const void* q, const void* v_src,
-                                   const void* k_src, uint32_t lds_v, uint32_t lds_k) {
+__device__ inline void decode_step(DecodeStepIo& io, int loading, int claiming, int* claim_ptr, const int32_t* bt0,
+                                   const int32_t* bt1, const void* q, const void* v_src0, const void* v_src1,
+                                   const void* k_src0, const void* k_src1, uint32_t lds_v, uint32_t lds_k) {
   uint64_t saved;
   uint32_t m0_saved;
   const int on_c = __builtin_amdgcn_readfirstlane(claiming != 0 ? 1 : 0);
   const int on_y = __builtin_amdgcn_readfirstlane(loading != 0 ? 1 : 0);
   lds_v = __builtin_amdgcn_readfirstlane(lds_v);
   lds_k = __builtin_amdgcn_readfirstlane(lds_k);
-  const char* v = (const char*)v_src;
-  const char* k = (const char*)k_src;
+  const char* v0 = (const char*)v_src0;
+  const char* v1 = (const char*)v_src1;
+  const char* k0 = (const char*)k_src0;
+  const char* k1 = (const char*)k_src1;
   if constexpr (kDma) {
     asm volatile(
         "s_mov_b64 %[sv], exec\n\t"
@@ -236,9 +244,9 @@ __device__ inline void decode_step(DecodeStepIo& io, int loading, int claiming, 
           [q0] "+v"(io.qv[0]), [q1] "+v"(io.qv[1]), [q2] "+v"(io.qv[2]), [q3] "+v"(io.qv[3]), [sv] "=&s"(saved),
           [m0s] "=&s"(m0_saved)
         : [onc] "s"(on_c), [ony] "s"(on_y), [cp] "v"(claim_ptr), [one] "v"(1),
-          [b0] "v"(bt0), [b1] "v"(bt1), [qp] "v"(q), [lv] "s"(lds_v), [lk] "s"(lds_k), [v0] "v"(v),
-          [v1] "v"(v + 64), [v2] "v"(v + 128), [v3] "v"(v + 192), [k0] "v"(k), [k1] "v"(k + 64),
-          [k2] "v"(k + 128), [k3] "v"(k + 192)
+          [b0] "v"(bt0), [b1] "v"(bt1), [qp] "v"(q), [lv] "s"(lds_v), [lk] "s"(lds_k), [v0] "v"(v0),
+          [v1] "v"(v1), [v2] "v"(v0 + 128), [v3] "v"(v1 + 128), [k0] "v"(k0), [k1] "v"(k1),
+          [k2] "v"(k0 + 128), [k3] "v"(k1 + 128)
         : "memory", "scc");
   } else {
     asm volatile(
@@ -456,12 +464,25 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds, int* p
   float m = -INFINITY;  // reference max of scaled scores (log2 domain), per g = c
   float l = 0.f;        // this lane's share of the running denominator
 
-  // Per-lane LDS offsets: K fragment (token c, chunk 4*q4 + j: byte
-  // (4*q4 + j)*256 + 16*c), and the transposed V read: lane c of group q4
-  // supplies token 4*q4 + c/4 at d 16*mt + 4*(c%4) (chunk 2*mt + (c%4)/2,
-  // byte 8*(c%2) inside it) and receives V[4*q4 + e][16*mt + c], e = 0..3.
-  const int koff = q4 * 1024 + c * 16;
-  const int voff = kDecodePageBytes + ((c >> 1) & 1) * 256 + (4 * q4 + (c >> 2)) * 16 + (c & 1) * 8;
+  // Per-lane addresses in the page layout of decode_step: the DMA sources
+  // (token lane/8, and 8 + lane/8, at chunk (lane%8) ^ swz), the K fragment
+  // of step j (token c, chunk 4*q4 + j) and the transposed V read: lane c of
+  // group q4 supplies token 4*q4 + c/4 at d 16*mt + 4*(c%4) (chunk
+  // 2*mt + (c%4)/2, byte 8*(c%2) inside it) and receives V[4*q4 + e][16*mt + c],
+  // e = 0..3; d-tiles mt and mt + 4 differ by 2 KB.
+  auto swz = [](int t) { return (2 * ((t >> 1) & 3)) | ((t >> 3) & 1); };
+  const int64_t src0_off = (int64_t)(lane >> 3) * p.tok_stride + 8 * ((lane & 7) ^ swz(lane >> 3));
+  const int64_t src1_off = (int64_t)(8 + (lane >> 3)) * p.tok_stride + 8 * ((lane & 7) ^ swz(8 + (lane >> 3)));
+  int koff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    koff[j] = (2 * (q4 >> 1) + (c >> 3)) * 1024 + (c & 7) * 128 + (((4 * (q4 & 1) + j) ^ swz(c)) * 16);
+  const int vtok = 4 * q4 + (c >> 2);
+  int voff[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    voff[m] = kDecodePageBytes + (vtok >> 3) * 1024 + (vtok & 7) * 128 +
+              (((2 * m + ((c >> 1) & 1)) ^ swz(vtok)) * 16) + (c & 1) * 8;
 
   // `edge` pages contain tokens past seq_len; the choice is wave-uniform.
   auto compute = [&](int pg, const lds_u8* buf, auto edge_tag) __attribute__((always_inline)) {
@@ -469,7 +490,7 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds, int* p
     f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      sc = Elem<T>::mfma16(lds_ld16<V8>(buf + koff + j * 256), q_lane ? __builtin_bit_cast(V8, qf[j]) : V8{}, sc);
+      sc = Elem<T>::mfma16(lds_ld16<V8>(buf + koff[j]), q_lane ? __builtin_bit_cast(V8, qf[j]) : V8{}, sc);
     // sc[r] = S[token 4*q4 + r][g = c]
     float tmax = -INFINITY;
 #pragma unroll
@@ -499,7 +520,7 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds, int* p
       pf[r] = (T)pr;
     }
     s16x4 vt[8];
-    lds_ld_tr16_x8_stride512(buf + voff, vt);
+    lds_ld_tr16_x8_4base(buf + voff[0], buf + voff[1], buf + voff[2], buf + voff[3], vt);
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
       s16x4 v = vt[mt];
@@ -589,11 +610,11 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds, int* p
     // X's first page, through the same asm path as every later page (the
     // compiler then tracks no LDS DMA at all in the loop).
     const int64_t base = (int64_t)page_of(bt_lo, bt_hi, 0) * p.page_stride + X[7] * kHeadDim;
-    const int64_t lane_off = (lane & 15) * p.tok_stride + 8 * (lane >> 4);
+    const T* vp = (const T*)p.v_cache + base;
+    const T* kp = (const T*)p.k_cache + base;
     const uint32_t lds_k = (uint32_t)(uintptr_t)lds;
-    decode_step<true>(io, 0, 0, claim_ctr, bt_word(X, lane), bt_word(X, 64 + lane), q_addr(X),
-                      (const T*)p.v_cache + base + lane_off, (const T*)p.k_cache + base + lane_off,
-                      lds_k + kDecodePageBytes, lds_k);
+    decode_step<true>(io, 0, 0, claim_ctr, bt_word(X, lane), bt_word(X, 64 + lane), q_addr(X), vp + src0_off,
+                      vp + src1_off, kp + src0_off, kp + src1_off, lds_k + kDecodePageBytes, lds_k);
   }
   int fvalid = 1;
   int fh = X[7], fpg = 0;
@@ -653,14 +674,15 @@ __device__ void decode_wave(const DecodeParams& p, int wave, lds_u8* lds, int* p
     const int taking = listed ? loading : claiming;
     if (fvalid) {
       const int64_t base = (int64_t)fpg * p.page_stride + fh * kHeadDim;
-      const int64_t lane_off = (lane & 15) * p.tok_stride + 8 * (lane >> 4);
+      const T* vp = (const T*)p.v_cache + base;
+      const T* kp = (const T*)p.k_cache + base;
       const uint32_t lds_k = (uint32_t)(uintptr_t)nxt;
-      decode_step<true>(io, loading, claiming, claim_ctr, bt_word(Y, lane), bt_word(Y, 64 + lane),
-                        q_addr(Y), (const T*)p.v_cache + base + lane_off, (const T*)p.k_cache + base + lane_off,
-                        lds_k + kDecodePageBytes, lds_k);
+      decode_step<true>(io, loading, claiming, claim_ctr, bt_word(Y, lane), bt_word(Y, 64 + lane), q_addr(Y),
+                        vp + src0_off, vp + src1_off, kp + src0_off, kp + src1_off, lds_k + kDecodePageBytes,
+                        lds_k);
     } else {
       decode_step<false>(io, loading, claiming, claim_ctr, bt_word(Y, lane), bt_word(Y, 64 + lane), q_addr(Y), nullptr,
-                         nullptr, 0, 0);
+                         nullptr, nullptr, nullptr, 0, 0);
     }
     wave_lds_fence();
     const int craw = io.claim;
