@@ -155,6 +155,34 @@ __device__ inline void dma16_x4_saddr(const void* base, uint32_t voff, uint32_t 
       : "memory", "scc");
 }
 
+// The same four copies for a page read as whole 128-byte lines: copy c moves
+// 16 bytes per lane from base + 128*(c/2) + (c%2 ? voff_b : voff_a) to LDS
+// byte address lds + 1024*c + 16*lane (voff_a addressing tokens 0-7 of a
+// page, voff_b tokens 8-15, 8 lanes per 128-byte line).
+__device__ inline void dma16_x4_lines(const void* base, uint32_t voff_a, uint32_t voff_b, uint32_t lds) {
+  uint32_t m0_saved;
+  const char* b = (const char*)base;
+  lds = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile(
+      "s_mov_b32 %[m0s], m0\n\t"
+      "s_mov_b32 m0, %[l]\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %[va], %[b0]\n\t"
+      "s_add_u32 m0, %[l], 0x400\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %[vb], %[b0]\n\t"
+      "s_add_u32 m0, %[l], 0x800\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %[va], %[b1]\n\t"
+      "s_add_u32 m0, %[l], 0xc00\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %[vb], %[b1]\n\t"
+      "s_mov_b32 m0, %[m0s]"
+      : [m0s] "=&s"(m0_saved)
+      : [l] "s"(lds), [va] "v"(voff_a), [vb] "v"(voff_b), [b0] "s"(b), [b1] "s"(b + 128)
+      : "memory", "scc");
+}
+
 // 16-byte global -> LDS copy; lane i's bytes land at lds_base + 16*i.
 __device__ inline void dma16(const void* g, lds_u8* lds_base) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);

@@ -63,8 +63,9 @@ struct PrefillParams {
   int out16;  // out and its strides are 16-byte aligned (16-byte output stores)
 };
 
-// LDS tile layouts.  A 64-key x 128-d tile is 16 blocks of 1 KB, block
-// (key/16, chunk/4) holding 16 keys x 4 16-byte d-chunks:
+// LDS tile layouts of the ping-pong kernel.  A 64-key x 128-d tile is 16
+// blocks of 1 KB, block (key/16, chunk/4) holding 16 keys x 4 16-byte
+// d-chunks:
 //   K: chunk-major inside a block, so the A-operand read of 16 consecutive
 //      keys at one chunk is 256 contiguous bytes;
 //   V: key-major inside a block, so a transposed read of 4 keys x 32 bytes by
@@ -76,6 +77,25 @@ __device__ inline int klds_off(int key, int ch) {
 }
 __device__ inline int vlds_blk_off(int key, int ch) {
   return (((key >> 4) << 2) + (ch >> 2)) * 1024 + (key & 15) * 64 + (ch & 3) * 16;
+}
+
+// Whole-line tile layouts (the MIXED kernel's prefill core).  A page slot
+// (16 keys, 4 KB) is 4 blocks of 1 KB, block 2 * (chunk / 8) + (key % 16) / 8
+// holding 8 keys x 128 contiguous bytes (chunks 8 * (chunk / 8) ..), so each
+// global_load_lds instruction reads whole cache lines.  The 16-byte chunk
+// order inside a key's 128 bytes is XOR-swizzled by key: for K so that 16
+// consecutive keys at one chunk cover all 64 banks (the A-operand read), for
+// V so that each 32-lane half of a transposed read (4 keys x 4 chunks x 2
+// halves) does.
+__device__ inline int line_kswz(int t) { return ((t >> 1) & 3) | ((t >> 3) << 2); }
+__device__ inline int line_vswz(int t) { return 4 * ((t >> 1) & 1); }
+__device__ inline int line_klds_off(int key, int ch) {
+  const int t = key & 15;
+  return (key >> 4) * 4096 + (2 * (ch >> 3) + (t >> 3)) * 1024 + (t & 7) * 128 + ((ch & 7) ^ line_kswz(t)) * 16;
+}
+__device__ inline int line_vlds_off(int key, int ch) {
+  return (key >> 4) * 4096 + (2 * (ch >> 3) + ((key >> 3) & 1)) * 1024 + (key & 7) * 128 +
+         ((ch & 7) ^ line_vswz(key & 7)) * 16;
 }
 
 // Max / sum of a value over the lane pair (l, l ^ 32): v_permlane32_swap
@@ -260,17 +280,20 @@ __device__ __attribute__((always_inline)) inline void prefill_core(const Prefill
     const int pg = sload(bt, min(tile * (kPrefillKeys / kPageSize) + w, npages - 1));
     return (pg >= 0 && pg < p.num_pages) ? pg : 0;
   };
-  // DMA of this wave's page of a K (or V) tile: 4 blocks of 1 KB.  Source =
-  // uniform page base + a 32-bit per-lane byte offset (+ 64 bytes per block).
-  //   K block cg: lane -> token lane%16, chunk 4*cg + lane/16
-  //   V block cg: lane -> token lane/4,  chunk 4*cg + lane%4
-  const uint32_t koff = (uint32_t)(((lane & 15) * p.tok_stride + 8 * (lane >> 4)) * (int64_t)sizeof(T));
-  const uint32_t voff = (uint32_t)(((lane >> 2) * p.tok_stride + 8 * (lane & 3)) * (int64_t)sizeof(T));
+  // DMA of this wave's page of a K (or V) tile in the whole-line layouts:
+  // lane -> token lane/8 (offset a) or 8 + lane/8 (offset b), chunk
+  // (lane % 8) ^ swizzle(token) of the 128-byte half the copy reads.
+  const uint32_t ts = (uint32_t)(p.tok_stride * (int64_t)sizeof(T));
+  const int lt = lane >> 3;
+  const uint32_t koff_a = (uint32_t)lt * ts + 16u * (uint32_t)((lane & 7) ^ line_kswz(lt));
+  const uint32_t koff_b = (uint32_t)(8 + lt) * ts + 16u * (uint32_t)((lane & 7) ^ line_kswz(8 + lt));
+  const uint32_t voff_a = (uint32_t)lt * ts + 16u * (uint32_t)((lane & 7) ^ line_vswz(lt));
+  const uint32_t voff_b = (uint32_t)(8 + lt) * ts + 16u * (uint32_t)((lane & 7) ^ line_vswz(lt));
   auto dma_k = [&](int page, lds_u8* buf) {
-    dma16_x4_saddr(kc + (int64_t)page * p.page_stride, koff, (uint32_t)(uintptr_t)(buf + 4096 * w));
+    dma16_x4_lines(kc + (int64_t)page * p.page_stride, koff_a, koff_b, (uint32_t)(uintptr_t)(buf + 4096 * w));
   };
   auto dma_v = [&](int page, lds_u8* buf) {
-    dma16_x4_saddr(vc + (int64_t)page * p.page_stride, voff, (uint32_t)(uintptr_t)(buf + 4096 * w));
+    dma16_x4_lines(vc + (int64_t)page * p.page_stride, voff_a, voff_b, (uint32_t)(uintptr_t)(buf + 4096 * w));
   };
 
   // The pipeline is written in issue order as steps of one MFMA each, its
@@ -284,18 +307,28 @@ __device__ __attribute__((always_inline)) inline void prefill_core(const Prefill
   // 4*hi + i%4] (the C layout of S^T = K Q^T).  Its probability goes to PV
   // k-step kk = 2*mt + (i/4)/2, word ((i/4) % 2)*2 + (i%4)/2 of pw[kk] (two
   // packed values per word: the B layout of P^T).
+  // QK step j: key 32*(j%2) + ln, chunk 2*(j/2) + hi; the swizzle makes the
+  // address a per-lane base (one per (j/2) % 4) plus an immediate.
+  int kbase[4];
+#pragma unroll
+  for (int c4 = 0; c4 < 4; ++c4) kbase[c4] = line_klds_off(ln, 2 * c4 + hi);
   auto kread = [&](const lds_u8* kb, int j) {  // QK step j: chain j % 2, k-step j / 2
-    return lds_ld16<V8>(kb + klds_off(32 * (j & 1) + ln, 2 * (j >> 1) + hi));
+    return lds_ld16<V8>(kb + kbase[(j >> 1) & 3] + 8192 * (j & 1) + 2048 * (j >> 3));
   };
   // PV step j: k-step j / 4, d-tile j % 4.  16-lane group a = lane/16 covers
   // d offset 16*(a&1) of the 32-d tile and keys 4*hi.. of each 8-key block;
-  // supplier lane ti gives row 4*hi + ti/4 at d offset 4*(ti%4).
+  // supplier lane ti gives row 4*hi + ti/4 at d offset 4*(ti%4), chunk
+  // 4*(j%4) + 2*(a&1) + (ti/2)%2 (two per-lane bases, by j % 2), and the
+  // same lanes give rows 8.. from the next block.
   const int ti = lane & 15;
   const int dgrp = (lane >> 4) & 1;
-  const int vlane_off = (4 * hi + (ti >> 2)) * 64 + (2 * dgrp + ((ti >> 1) & 1)) * 16 + (ti & 1) * 8;
+  const int vkey = 4 * hi + (ti >> 2);
+  const int vch = (2 * dgrp + ((ti >> 1) & 1)) ^ line_vswz(vkey);
+  const int vbase0 = vkey * 128 + vch * 16 + (ti & 1) * 8;
+  const int vbase1 = vkey * 128 + (vch ^ 4) * 16 + (ti & 1) * 8;
   auto vread = [&](const lds_u8* vb, int j) {
-    const lds_u8* a = vb + vlane_off + (j >> 2) * 4096 + (j & 3) * 1024;
-    return __builtin_bit_cast(V8, __builtin_shufflevector(lds_ld_tr16(a), lds_ld_tr16(a + 512), 0, 1, 2, 3, 4, 5, 6,
+    const lds_u8* a = vb + ((j & 1) ? vbase1 : vbase0) + (j >> 2) * 4096 + ((j >> 1) & 1) * 2048;
+    return __builtin_bit_cast(V8, __builtin_shufflevector(lds_ld_tr16(a), lds_ld_tr16(a + 1024), 0, 1, 2, 3, 4, 5, 6,
                                                           7));
   };
 
@@ -381,7 +414,7 @@ __device__ __attribute__((always_inline)) inline void prefill_core(const Prefill
     const int first_bad = kv - tile * kPrefillKeys;  // rows >= first_bad are past the sequence
     for (int i = tid; i < (kPrefillKeys - first_bad) * 16; i += 256) {
       const int key = first_bad + (i >> 4);
-      lds_st16<u32x4>(vb + vlds_blk_off(key, i & 15), u32x4{0, 0, 0, 0});
+      lds_st16<u32x4>(vb + line_vlds_off(key, i & 15), u32x4{0, 0, 0, 0});
     }
   };
 
