@@ -312,3 +312,28 @@ def test_output_only_8_byte_aligned_matches_aligned(gpu, dtype):
         outs.append(out.clone())
     assert torch.equal(outs[0], outs[1])
     assert_attention_close(outs[0].cpu(), expected(batch))
+
+
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (12, 4), (16, 1)])
+def test_padded_output_rows_match_contiguous(gpu, hq, hkv):
+    # Output rows at a padded, 16-byte aligned stride: the whole-line output
+    # stores address every row through the token and head strides, give the
+    # contiguous launch's bits and leave the padding untouched.
+    q = [300, 37, 130, 64, 1]
+    kv = [300 + 48, 37, 130 + 16, 64, 90]
+    batch = make_paged_batch(163, q, kv, len(q), hq, hkv)
+    common, qd, kc, vc = to_device(batch, gpu)
+    tile = ops.PREFILL_STREAM_ROWS // (hq // hkv)
+    n_tiles = len(_expected_tiles(q, kv, tile))
+    ws = torch.empty(ops.prefill_workspace_bytes(n_tiles), dtype=torch.uint8, device=gpu)
+    ref = torch.empty_like(qd)
+    ops.paged_prefill(qd, kc, vc, common.block_tables, common.seq_lens, common.query_start_loc, len(q), n_tiles,
+                      ws, ref, 128 ** -0.5)
+    padded = torch.full((qd.shape[0], hq, 136), float("nan"), dtype=qd.dtype, device=gpu)
+    out = padded[..., :128]
+    assert out.data_ptr() % 16 == 0 and (out.stride(0) * 2) % 16 == 0 and (out.stride(1) * 2) % 16 == 0
+    ops.paged_prefill(qd, kc, vc, common.block_tables, common.seq_lens, common.query_start_loc, len(q), n_tiles,
+                      ws, out, 128 ** -0.5)
+    assert torch.equal(out, ref)
+    assert bool(torch.isnan(padded[..., 128:]).all())
+    assert_attention_close(out.cpu(), expected(batch))
