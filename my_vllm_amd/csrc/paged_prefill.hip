@@ -26,8 +26,12 @@ namespace {
 // the format).  Sequences are ordered longest context first (batches of up
 // to kPrefillPlanSortMax sequences; larger batches keep batch order), and a
 // sequence's tiles largest key count first, so the tiles that read one
-// sequence's pages run together and long work starts early.  A sequence
-// with no queries, or with more queries than keys, gets no tile.  At most
+// sequence's pages run together and long work starts early.  The last
+// `tail` tiles (at most 1024) are then reordered by key count, largest
+// first (ties keep their order): they are the work the persistent grid
+// drains last, and without it a long tile of the last sequences could start
+// after the workgroups of its head had run out of work.  A sequence with no
+// queries, or with more queries than keys, gets no tile.  At most
 // `capacity` tiles are written; word 0 receives their number and word 1
 // the number left out.
 __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* __restrict__ qsl,
@@ -35,7 +39,7 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* __res
                                                             const int32_t* __restrict__ block_tables,
                                                             int64_t bt_stride, int64_t num_pages, int num_seqs,
                                                             int tile_tokens, int num_kv_heads,
-                                                            int32_t* __restrict__ plan, int capacity) {
+                                                            int32_t* __restrict__ plan, int capacity, int tail) {
   // Sequences in plan order (rank -> sequence) and the first tile of each
   // rank; beyond kPrefillPlanSortMax sequences, all keep batch order and are
   // planned in passes of kPrefillPlanSortMax.
@@ -125,6 +129,40 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* __res
       *reinterpret_cast<int4*>(d + 12) = int4{pg[4], pg[5], pg[6], pg[7]};
     }
     __syncthreads();
+  }
+  {
+    // The tail: thread i holds tile base + i, ranks it among the tail by key
+    // count (stable) and writes it to its rank.  Every thread has read its
+    // record (the barrier waits for the loads) before any is written.
+    const int n = min(carry, capacity);
+    const int K = min(min(n, tail), 1024);
+    if (K > 1) {
+      const int base = n - K;
+      int4 r0, r1, r2, r3;
+      int key = -1;
+      if (tid < K) {
+        const int4* src = reinterpret_cast<const int4*>(out + (int64_t)(base + tid) * kPrefillPlanItemInts);
+        r0 = src[0];
+        r1 = src[1];
+        r2 = src[2];
+        r3 = src[3];
+        key = r1.y;  // ntiles
+      }
+      scan[tid] = key;
+      __syncthreads();
+      if (tid < K) {
+        int rank = 0;
+        for (int o = 0; o < K; ++o) {
+          const int v = scan[o];
+          rank += (v > key) || (v == key && o < tid);
+        }
+        int4* dst = reinterpret_cast<int4*>(out + (int64_t)(base + rank) * kPrefillPlanItemInts);
+        dst[0] = r0;
+        dst[1] = r1;
+        dst[2] = r2;
+        dst[3] = r3;
+      }
+    }
   }
   if (tid == 0) {
     plan[0] = min(carry, capacity);
@@ -417,15 +455,17 @@ extern "C" int mva_paged_prefill(const void* q, int64_t q_token_stride, int64_t 
   int32_t* plan = (int32_t*)workspace;
   if (num_kv_heads > kPrefillPlanMaxHeads) return set_error("paged attention: at most 127 KV heads");
   p.tile_tokens = kPrefillPPRows / p.group;
-  hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(1024), 0, s, query_start_loc, seq_lens, block_tables,
-                     block_table_stride, num_pages, (int)num_seqs, p.tile_tokens, num_kv_heads, plan,
-                     (int)max_tiles);
-  rc = check_launch("paged_prefill plan");
-  if (rc) return rc;
   // Persistent grid: one workgroup per CU (96 KB of LDS and two waves per
   // SIMD each), a whole number per KV head, never more than the tiles can use.
   int64_t per_head = (int64_t)device_cu_count() / num_kv_heads;
   per_head = per_head < 1 ? 1 : (per_head > max_tiles ? max_tiles : per_head);
+  // The last three tiles per workgroup of a head go largest first.
+  const int tail = (int)(3 * per_head < 1024 ? 3 * per_head : 1024);
+  hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(1024), 0, s, query_start_loc, seq_lens, block_tables,
+                     block_table_stride, num_pages, (int)num_seqs, p.tile_tokens, num_kv_heads, plan,
+                     (int)max_tiles, tail);
+  rc = check_launch("paged_prefill plan");
+  if (rc) return rc;
   const dim3 grid((uint32_t)(per_head * num_kv_heads));
   if (dtype == kBF16)
     hipLaunchKernelGGL(paged_prefill_stream_kernel<__bf16>, grid, dim3(kPrefillPPThreads), 0, s, p, plan);
