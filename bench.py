@@ -91,6 +91,29 @@ def time_launches(fn, iters: int, warmup: int, repeats: int = 1) -> float:
     return statistics.median(per_call)
 
 
+def time_interleaved(fns, iters: int, warmup: int, repeats: int) -> list[float]:
+    """ms per call of each of `fns`, timed as time_launches does but in
+    alternating regions (the order reversed every other round), so that the
+    clock's swings under back-to-back MFMA work fall on all of them alike."""
+    for fn in fns:
+        for i in range(warmup):
+            fn(i)
+    torch.cuda.synchronize()
+    per_call = [[] for _ in fns]
+    for r in range(repeats):
+        order = range(len(fns)) if r % 2 == 0 else reversed(range(len(fns)))
+        for k in order:
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record()
+            for i in range(iters):
+                fns[k](i)
+            end.record()
+            torch.cuda.synchronize()
+            per_call[k].append(start.elapsed_time(end) / iters)
+    return [statistics.median(x) for x in per_call]
+
+
 def decode_bytes(batch, num_q_heads, num_kv_heads, elem=2) -> int:
     """Algorithmic bytes of one decode launch: unique K/V rows read, q read,
     o written, page ids and seq_lens read."""
@@ -300,12 +323,31 @@ def extra_measurements(device, steps: int):
 
     # PURE_PREFILL with prefix, Qwen3-8B.
     # The same CPU-seeded draw the parity tests check.
+    # The backend plans the tiles on a step's first layer and streams that
+    # plan on the others, so this is the per-layer time; prefill_with_plan_*
+    # is one launch that plans for itself (a one-layer step).
     batch = config_prefill(seed=2, device=device)
-    ms = attn_case(batch, 32, 8)
     flops = 4 * 128 * 32 * causal_pairs(batch.query_lengths, batch.kv_lengths)
+    backend = MI355XAttentionBackend(32, 8, 128, 16, torch.bfloat16)
+    common = to_device(batch, device)
+    plan = backend.build_plan(common)
+    md = plan.metadata
+    q, kc, vc = batch.q.to(device), batch.k_cache.to(device), batch.v_cache.to(device)
+    empty = q.new_empty((0, 8, 128))
+    out = torch.empty_like(q)
+    ws = torch.empty(ops.prefill_workspace_bytes(md.prefill_max_tiles), dtype=torch.uint8, device=device)
+    n_seqs = len(batch.query_lengths)
+    # Median of 9 regions of 20 launches each, the two in alternating regions.
+    ms, ms_plan = time_interleaved([
+        lambda i: backend.forward(q, empty, empty, kc, vc, plan),
+        lambda i: ops.paged_prefill(q, kc, vc, md.block_tables, md.seq_lens, md.query_start_loc, n_seqs,
+                                    md.prefill_max_tiles, ws, out, backend.softmax_scale, validate=False),
+    ], 20, 3, 9)
     res["prefill_TFLOPs"] = round(flops / ms / 1e9, 1)
     res["prefill_ms"] = round(ms, 4)
-    del batch
+    res["prefill_with_plan_TFLOPs"] = round(flops / ms_plan / 1e9, 1)
+    res["prefill_with_plan_ms"] = round(ms_plan, 4)
+    del batch, q, kc, vc, out, ws, backend, plan
 
     # MIXED, Qwen3-8B, token budget 8192.
     batch = config_mixed(seed=3, device=device)

@@ -373,6 +373,33 @@ int mva_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_stri
                       int page_size, float softmax_scale, int dtype, void* stream);
 
 /*
+ * mva_paged_prefill in two parts, for a step whose layers share one batch:
+ * mva_paged_prefill_plan builds the tile list of the batch into `workspace`
+ * once, and mva_paged_prefill_run then streams it for each layer's q, caches
+ * and out (arguments as mva_paged_prefill).  A run needs the plan that
+ * mva_paged_prefill_plan (or mva_paged_prefill) wrote into the same workspace
+ * for the same block_tables, seq_lens, query_start_loc, num_seqs, max_tiles
+ * and head counts, with none of them changed since; each run leaves the plan
+ * ready for the next.  Both are ordered by `stream` and must not overlap
+ * other launches on the workspace.  The dropped-tile word is written by the
+ * plan.  Mirror the reference's once-per-step FlashInfer
+ * BatchPrefillWithPagedKVCacheWrapper.plan (nanovllm/layers/attention_backend.py:810-825,
+ * from build_plan :769-894) and its per-layer run (:992-994).
+ */
+int mva_paged_prefill_plan(const int32_t* block_tables, int64_t block_table_stride, int64_t num_pages,
+                           const int32_t* seq_lens, const int32_t* query_start_loc, int64_t num_seqs,
+                           int64_t max_tiles, void* workspace, int64_t workspace_bytes, int num_q_heads,
+                           int num_kv_heads, void* stream);
+int mva_paged_prefill_run(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                          const void* k_cache, const void* v_cache, int64_t num_pages,
+                          int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
+                          int64_t block_table_stride, const int32_t* seq_lens,
+                          const int32_t* query_start_loc, int64_t num_seqs, int64_t max_tiles,
+                          void* workspace, int64_t workspace_bytes, void* out, int64_t out_token_stride,
+                          int64_t out_head_stride, int num_q_heads, int num_kv_heads, int head_dim,
+                          int page_size, float softmax_scale, int dtype, void* stream);
+
+/*
  * MIXED batch in one launch: prefill tiles write the rows of the leading
  * num_prefill_seqs (<= 1024) sequences and decode pieces (as
  * mva_paged_decode, claim schedule) write the trailing decode rows of the

@@ -146,6 +146,25 @@ _SIGNATURES = {
             _i32, _i32, _i32, _i32, _f32, _i32, _c_void_p,
         ],
     ),
+    "mva_paged_prefill_plan": (
+        _i32,
+        [
+            _c_void_p, _i64, _i64,  # block_tables, stride, num_pages
+            _c_void_p, _c_void_p, _i64, _i64,  # seq_lens, query_start_loc, num_seqs, max_tiles
+            _c_void_p, _i64, _i32, _i32, _c_void_p,  # workspace, workspace_bytes, heads, stream
+        ],
+    ),
+    "mva_paged_prefill_run": (
+        _i32,
+        [
+            _c_void_p, _i64, _i64,
+            _c_void_p, _c_void_p, _i64, _i64, _i64,
+            _c_void_p, _i64, _c_void_p, _c_void_p,
+            _i64, _i64, _c_void_p, _i64,
+            _c_void_p, _i64, _i64,
+            _i32, _i32, _i32, _i32, _f32, _i32, _c_void_p,
+        ],
+    ),
     "mva_paged_mixed": (
         _i32,
         [
@@ -163,7 +182,7 @@ _SIGNATURES = {
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 # The C ABI revision these signatures describe (mva_abi_version()).
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -504,6 +504,9 @@ class MI355XAttentionBackendMixin:
         self._output_buffer: torch.Tensor | None = None
         self._workspace: torch.Tensor | None = None
         self._prefill_workspace: torch.Tensor | None = None
+        # The metadata whose device tile plan the prefill workspace holds:
+        # the first prefill launch of a step plans, the other layers reuse it.
+        self._prefill_planned_for: MI355XAttentionMetadata | None = None
         self._staging = PinnedStaging()
         self._active_graph_state: MI355XFullDecodeGraphState | None = None
         # (key, value, slot_mapping) of the step while forward_with_kv_store
@@ -761,6 +764,7 @@ class MI355XAttentionBackendMixin:
                 or "the MIXED metadata was planned for prefill + decode launches"
             )
         plan = self.plan_type(batch_type, route, common, metadata)
+        self._prefill_planned_for = None  # a new step plans its prefill tiles again
         self._planned_route = route.value
         self._route_counts[route.value] += 1
         return plan
@@ -786,6 +790,7 @@ class MI355XAttentionBackendMixin:
         if ws is None or ws.numel() < nbytes or ws.device != device:
             ws = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
             self._prefill_workspace = ws
+            self._prefill_planned_for = None
         return ws
 
     def _get_workspace(self, nbytes: int, device: torch.device) -> torch.Tensor | None:
@@ -1139,8 +1144,14 @@ class MI355XAttentionBackendMixin:
         max_tiles = ops.prefill_max_tiles(q.size(0), q_lens.size, self.num_q_heads, self.num_kv_heads)
         ops.paged_prefill(q, pool[0], pool[1], block_tables, seq_lens, common.query_start_loc, q_lens.size,
                           max_tiles, self._get_prefill_workspace(max_tiles, device), output, self.softmax_scale)
+        self._prefill_planned_for = None
 
     def _run_prefill(self, q, k_cache, v_cache, common, metadata: MI355XAttentionMetadata, output) -> None:
+        # The tile plan depends on the batch only: the first launch for this
+        # metadata builds it on the device, later layers stream it as it is
+        # (the reference's FlashInfer wrapper plans once per step in build_plan,
+        # nanovllm/layers/attention_backend.py:810-825, and runs per layer, :992-994).
+        workspace = self._get_prefill_workspace(metadata.prefill_max_tiles, q.device)
         ops.paged_prefill(
             q,
             k_cache,
@@ -1150,10 +1161,12 @@ class MI355XAttentionBackendMixin:
             metadata.query_start_loc,
             common.num_prefill_seqs,
             metadata.prefill_max_tiles,
-            self._get_prefill_workspace(metadata.prefill_max_tiles, q.device),
+            workspace,
             output,
             self.softmax_scale,
+            planned=self._prefill_planned_for is metadata,
         )
+        self._prefill_planned_for = metadata
 
     def _run_mixed(self, q, k_cache, v_cache, common, metadata: MI355XAttentionMetadata, output) -> None:
         group = self.num_q_heads // self.num_kv_heads

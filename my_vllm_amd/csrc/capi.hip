@@ -27,4 +27,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* mva_last_error(void) { return mva::g_last_error; }
 
-extern "C" int mva_abi_version(void) { return 10; }
+extern "C" int mva_abi_version(void) { return 11; }

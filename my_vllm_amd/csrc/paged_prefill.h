@@ -549,9 +549,15 @@ __device__ __attribute__((always_inline)) inline void prefill_core(const Prefill
 constexpr int kPrefillPlanItemInts = 16;
 // Header: word 0 = tile count (at most the capacity); word 1 = tiles of the
 // batch beyond the capacity, which are not run (0 when the capacity bounds
-// the batch); the claim counter of KV head h at word
-// kPrefillPlanLineInts * (1 + h), each on its own 128-byte line.
+// the batch); word 16 = workgroups of the running launch that have finished;
+// word 17 = workgroups of the launches that stream the plan; the claim
+// counter of KV head h at word kPrefillPlanLineInts * (1 + h), each on its
+// own 128-byte line.  The planner zeroes the counters and the last
+// workgroup of every launch zeroes them again, so one plan serves any number
+// of launches in stream order.
 constexpr int kPrefillPlanDroppedInt = 1;
+constexpr int kPrefillPlanExitInt = 16;
+constexpr int kPrefillPlanGridInt = 17;
 constexpr int kPrefillPlanLineInts = 32;
 constexpr int kPrefillPlanMaxHeads = 127;
 constexpr int kPrefillPlanHeaderInts = kPrefillPlanLineInts * (1 + kPrefillPlanMaxHeads);

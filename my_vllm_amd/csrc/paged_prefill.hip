@@ -39,7 +39,8 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* __res
                                                             const int32_t* __restrict__ block_tables,
                                                             int64_t bt_stride, int64_t num_pages, int num_seqs,
                                                             int tile_tokens, int num_kv_heads,
-                                                            int32_t* __restrict__ plan, int capacity, int tail) {
+                                                            int32_t* __restrict__ plan, int capacity, int tail,
+                                                            int grid) {
   // Sequences in plan order (rank -> sequence) and the first tile of each
   // rank; beyond kPrefillPlanSortMax sequences, all keep batch order and are
   // planned in passes of kPrefillPlanSortMax.
@@ -167,6 +168,8 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* __res
   if (tid == 0) {
     plan[0] = min(carry, capacity);
     plan[kPrefillPlanDroppedInt] = max(carry - capacity, 0);
+    plan[kPrefillPlanExitInt] = 0;
+    plan[kPrefillPlanGridInt] = grid;
   }
   if (tid < num_kv_heads) plan[kPrefillPlanLineInts * (1 + tid)] = 0;  // claim counters
 }
@@ -187,6 +190,25 @@ __global__ __launch_bounds__(kPrefillPPThreads) void paged_prefill_stream_kernel
     prefill_items_pingpong<T, 0>(p, plan, h, (lds_u8*)tiles, (lds_i32*)nextq);
   else
     prefill_items_pingpong<T, 1>(p, plan, h, (lds_u8*)tiles, (lds_i32*)nextq);
+  // The last workgroup out zeroes the claim counters and the exit count, so
+  // the plan serves the next launch as it is.  Every claim and counter read
+  // of a workgroup has returned (its result decided the exit) before thread 0
+  // counts the workgroup out, and workgroups of any head claim from every
+  // head's counter, so only the grid's last exit may clear them.
+  // (The grid size comes from the plan header, which keeps the dispatch
+  // packet's registers out of the tile loop.)
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    int gone = 0;
+    if (threadIdx.x == 0)
+      gone = __hip_atomic_fetch_add(plan + kPrefillPlanExitInt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    gone = __builtin_amdgcn_readfirstlane(gone);
+    if (gone == plan[kPrefillPlanGridInt] - 1) {
+      for (int hh = threadIdx.x; hh < kPrefillPlanMaxHeads; hh += 64)
+        __hip_atomic_store(plan + kPrefillPlanLineInts * (1 + hh), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (threadIdx.x == 0) __hip_atomic_store(plan + kPrefillPlanExitInt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 int device_cu_count() {
@@ -429,14 +451,17 @@ extern "C" int64_t mva_prefill_workspace_bytes(int64_t max_tiles) {
   return (mva::kPrefillPlanHeaderInts + max_tiles * mva::kPrefillPlanItemInts) * 4;
 }
 
-extern "C" int mva_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_stride,
-                                 const void* k_cache, const void* v_cache, int64_t num_pages,
-                                 int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
-                                 int64_t block_table_stride, const int32_t* seq_lens,
-                                 const int32_t* query_start_loc, int64_t num_seqs, int64_t max_tiles,
-                                 void* workspace, int64_t workspace_bytes, void* out, int64_t out_token_stride,
-                                 int64_t out_head_stride, int num_q_heads, int num_kv_heads, int head_dim,
-                                 int page_size, float softmax_scale, int dtype, void* stream) {
+namespace {
+
+// Plans (plan_it) and/or streams (run_it) a prefill batch: the shared body
+// of mva_paged_prefill, mva_paged_prefill_plan and mva_paged_prefill_run.
+int prefill_launch(const void* q, int64_t q_token_stride, int64_t q_head_stride, const void* k_cache,
+                   const void* v_cache, int64_t num_pages, int64_t page_stride, int64_t token_stride,
+                   const int32_t* block_tables, int64_t block_table_stride, const int32_t* seq_lens,
+                   const int32_t* query_start_loc, int64_t num_seqs, int64_t max_tiles, void* workspace,
+                   int64_t workspace_bytes, void* out, int64_t out_token_stride, int64_t out_head_stride,
+                   int num_q_heads, int num_kv_heads, int head_dim, int page_size, float softmax_scale, int dtype,
+                   void* stream, bool plan_it, bool run_it) {
   using namespace mva;
   PrefillParams p;
   int rc = fill_prefill_params(p, q, q_token_stride, q_head_stride, k_cache, v_cache, num_pages, page_stride,
@@ -459,19 +484,68 @@ extern "C" int mva_paged_prefill(const void* q, int64_t q_token_stride, int64_t 
   // SIMD each), a whole number per KV head, never more than the tiles can use.
   int64_t per_head = (int64_t)device_cu_count() / num_kv_heads;
   per_head = per_head < 1 ? 1 : (per_head > max_tiles ? max_tiles : per_head);
-  // The last three tiles per workgroup of a head go largest first.
-  const int tail = (int)(3 * per_head < 1024 ? 3 * per_head : 1024);
-  hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(1024), 0, s, query_start_loc, seq_lens, block_tables,
-                     block_table_stride, num_pages, (int)num_seqs, p.tile_tokens, num_kv_heads, plan,
-                     (int)max_tiles, tail);
-  rc = check_launch("paged_prefill plan");
-  if (rc) return rc;
+  if (plan_it) {
+    // The last three tiles per workgroup of a head go largest first.
+    const int tail = (int)(3 * per_head < 1024 ? 3 * per_head : 1024);
+    hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(1024), 0, s, query_start_loc, seq_lens, block_tables,
+                       block_table_stride, num_pages, (int)num_seqs, p.tile_tokens, num_kv_heads, plan,
+                       (int)max_tiles, tail, (int)(per_head * num_kv_heads));
+    rc = check_launch("paged_prefill plan");
+    if (rc) return rc;
+  }
+  if (!run_it) return 0;
   const dim3 grid((uint32_t)(per_head * num_kv_heads));
   if (dtype == kBF16)
     hipLaunchKernelGGL(paged_prefill_stream_kernel<__bf16>, grid, dim3(kPrefillPPThreads), 0, s, p, plan);
   else
     hipLaunchKernelGGL(paged_prefill_stream_kernel<_Float16>, grid, dim3(kPrefillPPThreads), 0, s, p, plan);
   return check_launch("paged_prefill");
+}
+
+// Stand-ins for the buffers a plan-only launch does not touch: they pass the
+// alignment checks and are never dereferenced.
+alignas(16) const uint8_t kPlanOnlyDummy[16] = {};
+
+}  // namespace
+
+extern "C" int mva_paged_prefill(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                                 const void* k_cache, const void* v_cache, int64_t num_pages,
+                                 int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
+                                 int64_t block_table_stride, const int32_t* seq_lens,
+                                 const int32_t* query_start_loc, int64_t num_seqs, int64_t max_tiles,
+                                 void* workspace, int64_t workspace_bytes, void* out, int64_t out_token_stride,
+                                 int64_t out_head_stride, int num_q_heads, int num_kv_heads, int head_dim,
+                                 int page_size, float softmax_scale, int dtype, void* stream) {
+  return prefill_launch(q, q_token_stride, q_head_stride, k_cache, v_cache, num_pages, page_stride, token_stride,
+                        block_tables, block_table_stride, seq_lens, query_start_loc, num_seqs, max_tiles, workspace,
+                        workspace_bytes, out, out_token_stride, out_head_stride, num_q_heads, num_kv_heads, head_dim,
+                        page_size, softmax_scale, dtype, stream, true, true);
+}
+
+extern "C" int mva_paged_prefill_plan(const int32_t* block_tables, int64_t block_table_stride, int64_t num_pages,
+                                      const int32_t* seq_lens, const int32_t* query_start_loc, int64_t num_seqs,
+                                      int64_t max_tiles, void* workspace, int64_t workspace_bytes,
+                                      int num_q_heads, int num_kv_heads, void* stream) {
+  const void* d = kPlanOnlyDummy;
+  return prefill_launch(d, 0, 0, d, d, num_pages, 0, 0, block_tables, block_table_stride, seq_lens,
+                        query_start_loc, num_seqs, max_tiles, workspace, workspace_bytes, (void*)d, 0, 0,
+                        num_q_heads, num_kv_heads, mva::kHeadDim, mva::kPageSize, 1.0f, mva::kBF16, stream, true,
+                        false);
+}
+
+extern "C" int mva_paged_prefill_run(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                                     const void* k_cache, const void* v_cache, int64_t num_pages,
+                                     int64_t page_stride, int64_t token_stride, const int32_t* block_tables,
+                                     int64_t block_table_stride, const int32_t* seq_lens,
+                                     const int32_t* query_start_loc, int64_t num_seqs, int64_t max_tiles,
+                                     void* workspace, int64_t workspace_bytes, void* out,
+                                     int64_t out_token_stride, int64_t out_head_stride, int num_q_heads,
+                                     int num_kv_heads, int head_dim, int page_size, float softmax_scale, int dtype,
+                                     void* stream) {
+  return prefill_launch(q, q_token_stride, q_head_stride, k_cache, v_cache, num_pages, page_stride, token_stride,
+                        block_tables, block_table_stride, seq_lens, query_start_loc, num_seqs, max_tiles, workspace,
+                        workspace_bytes, out, out_token_stride, out_head_stride, num_q_heads, num_kv_heads, head_dim,
+                        page_size, softmax_scale, dtype, stream, false, true);
 }
 
 extern "C" int mva_paged_mixed(const void* q, int64_t q_token_stride, int64_t q_head_stride,

@@ -661,6 +661,7 @@ def paged_prefill(
     softmax_scale: float,
     *,
     validate: bool = True,
+    planned: bool = False,
 ) -> None:
     """Launch the ragged causal prefill over the first ``num_seqs`` sequences.
 
@@ -669,19 +670,50 @@ def paged_prefill(
     ``prefill_workspace_bytes(max_tiles)`` bytes); ``max_tiles`` must bound
     the tile count (see :func:`prefill_max_tiles`): tiles beyond it are not
     run and counted at :data:`PREFILL_DROPPED_TILES_OFFSET`
-    (:func:`prefill_dropped_tiles`).
+    (:func:`prefill_dropped_tiles`).  With ``planned=True`` the launch
+    streams the plan that :func:`paged_prefill_plan` (or an earlier launch)
+    left in ``workspace`` for the same batch metadata, and plans nothing.
     """
     if validate:
         _check_paged(q, out, k_cache, v_cache,
                      (("block_tables", block_tables), ("seq_lens", seq_lens), ("query_start_loc", query_start_loc)),
                      (("workspace", workspace),))
     _native.call(
-        "mva_paged_prefill",
+        "mva_paged_prefill_run" if planned else "mva_paged_prefill",
         *_paged_args(q, k_cache, v_cache, block_tables, seq_lens),
         query_start_loc.data_ptr(), int(num_seqs), int(max_tiles),
         workspace.data_ptr(), workspace.numel() * workspace.element_size(),
         out.data_ptr(), out.stride(0), out.stride(1),
         *_tail_args(q, k_cache, softmax_scale),
+    )
+
+
+def paged_prefill_plan(
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    query_start_loc: torch.Tensor,
+    num_seqs: int,
+    max_tiles: int,
+    workspace: torch.Tensor,
+    num_pages: int,
+    num_q_heads: int,
+    num_kv_heads: int,
+) -> None:
+    """Build the tile list of a prefill batch into ``workspace`` on the
+    current stream of the workspace's device, once for the layers of a step;
+    each layer then calls :func:`paged_prefill` with ``planned=True``.  Plans
+    and launches on one workspace must not overlap."""
+    for name, t in (("block_tables", block_tables), ("seq_lens", seq_lens), ("query_start_loc", query_start_loc)):
+        if t.device != workspace.device or t.dtype != torch.int32:
+            raise RuntimeError(f"{name} must be an int32 tensor on the workspace's device")
+    if seq_lens.stride(0) != 1 or query_start_loc.stride(0) != 1 or block_tables.stride(1) != 1:
+        raise RuntimeError("seq_lens, query_start_loc and block table rows must be dense")
+    _native.call(
+        "mva_paged_prefill_plan",
+        block_tables.data_ptr(), block_tables.stride(0), int(num_pages),
+        seq_lens.data_ptr(), query_start_loc.data_ptr(), int(num_seqs), int(max_tiles),
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+        int(num_q_heads), int(num_kv_heads), _native.stream_handle(workspace.device),
     )
 
 

@@ -7,6 +7,8 @@ single-token chunk with a long context, unaligned prefixes, NaN-poisoned
 stale rows, fp16, trusted vs untrusted metadata, and the cacheless warmup.
 """
 
+import dataclasses
+
 import pytest
 import torch
 
@@ -343,3 +345,68 @@ def test_padded_output_rows_match_contiguous(gpu, hq, hkv):
     assert torch.equal(out, ref)
     assert bool(torch.isnan(padded[..., 128:]).all())
     assert_attention_close(out.cpu(), expected(batch))
+
+
+def _layers(seed, q, kv, hq, hkv, n):
+    """n batches with one step's lengths and pages and each layer's own
+    queries and cache values."""
+    base = make_paged_batch(seed, q, kv, len(q), hq, hkv)
+    out = [base]
+    for i in range(1, n):
+        g = torch.Generator().manual_seed(seed * 100 + i)
+        new = lambda t: torch.randn(t.shape, generator=g).to(t.dtype)  # noqa: E731
+        out.append(dataclasses.replace(base, q=new(base.q), k_cache=new(base.k_cache), v_cache=new(base.v_cache)))
+    return out
+
+
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (16, 1)])
+def test_one_plan_serves_every_layer(gpu, hq, hkv):
+    # One device plan, then a run per layer with that layer's queries and
+    # caches: each run gives the bits of a launch that plans for itself, and
+    # leaves the claim counters and the exit count at zero for the next.
+    q = [300, 37, 130, 64, 1, 700]
+    kv = [300 + 48, 37, 130 + 16, 64, 90, 900]
+    layers = _layers(170, q, kv, hq, hkv, 3)
+    common, _, _, _ = to_device(layers[0], gpu)
+    tile = ops.PREFILL_STREAM_ROWS // (hq // hkv)
+    n_tiles = len(_expected_tiles(q, kv, tile))
+    ws = torch.empty(ops.prefill_workspace_bytes(n_tiles), dtype=torch.uint8, device=gpu)
+    ws_fresh = torch.empty_like(ws)
+    num_pages = layers[0].k_cache.shape[0]
+    ops.paged_prefill_plan(common.block_tables, common.seq_lens, common.query_start_loc, len(q), n_tiles, ws,
+                           num_pages, hq, hkv)
+    scale = 128 ** -0.5
+    for batch in layers:
+        _, qd, kc, vc = to_device(batch, gpu)
+        out = torch.full_like(qd, float("nan"))
+        ops.paged_prefill(qd, kc, vc, common.block_tables, common.seq_lens, common.query_start_loc, len(q), n_tiles,
+                          ws, out, scale, planned=True)
+        ref = torch.full_like(qd, float("nan"))
+        ops.paged_prefill(qd, kc, vc, common.block_tables, common.seq_lens, common.query_start_loc, len(q), n_tiles,
+                          ws_fresh, ref, scale)
+        assert torch.equal(out, ref)
+        header = ws[:ops.PREFILL_PLAN_HEADER_INTS * 4].view(torch.int32).cpu()
+        assert int(header[0]) == n_tiles and int(header[1]) == 0
+        assert int(header[16]) == 0  # exit count
+        lines = header[32:].view(-1, 32)[:, 0]
+        assert int(lines.abs().sum()) == 0  # claim counters
+        assert_attention_close(out.cpu(), expected(batch))
+
+
+def test_backend_plans_prefill_tiles_once_per_step(gpu):
+    # The PREFILL route plans on its first layer and streams that plan on the
+    # next; a new step (build_plan) plans again, also for a batch whose
+    # lengths differ.
+    hq, hkv = 32, 8
+    backend = MI355XAttentionBackend(hq, hkv, 128, 16, torch.bfloat16)
+    for step, (q, kv) in enumerate([([300, 37, 130], [348, 37, 146]), ([64, 700], [64, 900])]):
+        layers = _layers(180 + step, q, kv, hq, hkv, 2)
+        common, _, _, _ = to_device(layers[0], gpu)
+        plan = backend.build_plan(common)
+        assert backend._prefill_planned_for is None
+        for batch in layers:
+            _, qd, kc, vc = to_device(batch, gpu)
+            empty = qd.new_empty((0, hkv, 128))
+            out = backend.forward(qd, empty, empty, kc, vc, plan).clone()
+            assert backend._prefill_planned_for is plan.metadata
+            assert_attention_close(out.cpu(), expected(batch))
