@@ -71,6 +71,16 @@ def test_invalid_arguments_fail_before_launch_with_a_message():
     with pytest.raises(RuntimeError, match="at most 1024 prefill sequences"):
         _native.call("mva_paged_mixed", 0, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0, 1025, 2000, 0, 0, 0, 0,
                      0, 0, 0, 0, 0, 16, 8, 128, 16, 1.0, 0, 0)
+    # The prefill plan and run entry points check heads and the workspace
+    # before they touch the device; an empty batch is a no-op.
+    with pytest.raises(RuntimeError, match="positive multiple of num_kv_heads"):
+        _native.call("mva_paged_prefill_plan", 0, 0, 1, 0, 0, 1, 1, 0, 0, 12, 8, 0)
+    with pytest.raises(RuntimeError, match="prefill workspace too small"):
+        _native.call("mva_paged_prefill_plan", 0, 0, 1, 0, 0, 1, 1, 0, 0, 32, 8, 0)
+    _native.call("mva_paged_prefill_plan", 0, 0, 1, 0, 0, 0, 1, 0, 0, 32, 8, 0)
+    with pytest.raises(RuntimeError, match="prefill workspace too small"):
+        _native.call("mva_paged_prefill_run", 0, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0, 1, 1, 0, 0, 0, 0, 0,
+                     32, 8, 128, 16, 1.0, 0, 0)
 
 
 def test_dtype_codes_match_the_header():
