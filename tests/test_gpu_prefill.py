@@ -347,10 +347,10 @@ def test_padded_output_rows_match_contiguous(gpu, hq, hkv):
     assert_attention_close(out.cpu(), expected(batch))
 
 
-def _layers(seed, q, kv, hq, hkv, n):
+def _layers(seed, q, kv, hq, hkv, n, num_prefill=None):
     """n batches with one step's lengths and pages and each layer's own
     queries and cache values."""
-    base = make_paged_batch(seed, q, kv, len(q), hq, hkv)
+    base = make_paged_batch(seed, q, kv, len(q) if num_prefill is None else num_prefill, hq, hkv)
     out = [base]
     for i in range(1, n):
         g = torch.Generator().manual_seed(seed * 100 + i)
@@ -410,3 +410,22 @@ def test_backend_plans_prefill_tiles_once_per_step(gpu):
             out = backend.forward(qd, empty, empty, kc, vc, plan).clone()
             assert backend._prefill_planned_for is plan.metadata
             assert_attention_close(out.cpu(), expected(batch))
+
+
+def test_split_mixed_route_reuses_the_prefill_plan_across_layers(gpu):
+    # MIXED_SPLIT: the prefill half plans on the first layer and streams the
+    # same plan on the next; both layers match the oracle, decode rows too.
+    hq, hkv = 32, 8
+    q = [300, 37, 130, 1, 1, 1]
+    kv = [348, 37, 146, 90, 700, 17]
+    backend = MI355XAttentionBackend(hq, hkv, 128, 16, torch.bfloat16, attention_mode="split")
+    layers = _layers(190, q, kv, hq, hkv, 2, num_prefill=3)
+    common, _, _, _ = to_device(layers[0], gpu)
+    plan = backend.build_plan(common)
+    assert plan.route is AttentionRoute.MIXED_SPLIT
+    for batch in layers:
+        _, qd, kc, vc = to_device(batch, gpu)
+        empty = qd.new_empty((0, hkv, 128))
+        out = backend.forward(qd, empty, empty, kc, vc, plan).clone()
+        assert backend._prefill_planned_for is plan.metadata
+        assert_attention_close(out.cpu(), expected(batch))
