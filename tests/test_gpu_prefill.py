@@ -359,8 +359,8 @@ def _layers(seed, q, kv, hq, hkv, n, num_prefill=None):
     return out
 
 
-@pytest.mark.parametrize("hq,hkv", [(32, 8), (16, 1)])
-def test_one_plan_serves_every_layer(gpu, hq, hkv):
+@pytest.mark.parametrize("hq,hkv,dtype", [(32, 8, torch.bfloat16), (16, 1, torch.bfloat16), (12, 4, torch.float16)])
+def test_one_plan_serves_every_layer(gpu, hq, hkv, dtype):
     # One device plan, then a run per layer with that layer's queries and
     # caches: each run gives the bits of a launch that plans for itself, and
     # leaves the claim counters and the exit count at zero for the next.
@@ -377,7 +377,7 @@ def test_one_plan_serves_every_layer(gpu, hq, hkv):
                            num_pages, hq, hkv)
     scale = 128 ** -0.5
     for batch in layers:
-        _, qd, kc, vc = to_device(batch, gpu)
+        _, qd, kc, vc = (x.to(dtype) if torch.is_tensor(x) else x for x in to_device(batch, gpu))
         out = torch.full_like(qd, float("nan"))
         ops.paged_prefill(qd, kc, vc, common.block_tables, common.seq_lens, common.query_start_loc, len(q), n_tiles,
                           ws, out, scale, planned=True)
@@ -390,7 +390,9 @@ def test_one_plan_serves_every_layer(gpu, hq, hkv):
         assert int(header[16]) == 0  # exit count
         lines = header[32:].view(-1, 32)[:, 0]
         assert int(lines.abs().sum()) == 0  # claim counters
-        assert_attention_close(out.cpu(), expected(batch))
+        want = expected(dataclasses.replace(batch, q=batch.q.to(dtype), k_cache=batch.k_cache.to(dtype),
+                                            v_cache=batch.v_cache.to(dtype)))
+        assert_attention_close(out.cpu(), want)
 
 
 def test_backend_plans_prefill_tiles_once_per_step(gpu):
